@@ -1,0 +1,155 @@
+/*
+ * uor_gfx950.h -- the C ABI of the MI355X (gfx950) route for the
+ * exact-accumulation GEMM hot path of UOR-Foundation/uor-matmul.
+ *
+ * Every entry point computes exactly what the reference's CPU routes compute,
+ * byte for byte: the exact sum, scaled and combined in the accumulator's width,
+ * encoded once into the requested output type.
+ *
+ * Conventions (all entry points):
+ *   - Every operand, output and scratch pointer is a DEVICE pointer owned by
+ *     the caller.  The library never allocates device or pinned memory on the
+ *     call path; `scratch` is an offer of any size, including 0, and changes
+ *     only which kernels run, never the bytes written (reference CD-10,
+ *     crates/uor-matmul-gemm/src/scratch.rs:50-120).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL is the default
+ *     stream) and the call returns without synchronising.  Shape validation
+ *     happens on the host before anything is enqueued.
+ *   - Strides are in elements and may be negative or zero on inputs, exactly
+ *     as the reference's Strides (crates/uor-matmul-core/src/layout.rs:29-154).
+ *   - Status: 0 ok; the reference's two NotAProduct variants
+ *     (crates/uor-matmul-core/src/error.rs:28-53) as 1 and 2; a buffer that
+ *     does not hold the view its caller described (MatView::new -> None,
+ *     layout.rs:212; the slice face's does_not_fit panic, slice.rs:104-116)
+ *     as 3; an argument outside the enums below as 4; a HIP runtime failure
+ *     as 100 + hipError_t (device-only; the reference has no such state).
+ *     Values, depth and magnitude never produce an error (reference CT-01,
+ *     CT-05).
+ */
+#ifndef UOR_GFX950_H
+#define UOR_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+#define UOR_OK 0
+#define UOR_NONCONFORMANT 1          /* NotAProduct::Nonconformant */
+#define UOR_OUTPUT_ALIASES_ITSELF 2  /* NotAProduct::OutputAliasesItself */
+#define UOR_SHORT_BUFFER 3           /* a view does not fit its buffer */
+#define UOR_INVALID_ARGUMENT 4       /* unknown enum value */
+#define UOR_HIP_ERROR 100            /* + hipError_t */
+
+/* EncodeMode, crates/uor-matmul-core/src/policy.rs:19-43.  The slice face
+ * always uses UOR_ENCODE_NEAREST (GemmOptions::default()). */
+#define UOR_ENCODE_NEAREST 0
+#define UOR_ENCODE_TOWARD_ZERO 1
+#define UOR_ENCODE_SATURATING 2
+#define UOR_ENCODE_WRAPPING 3
+
+/* Integer output element type O, named by its width in bytes
+ * (EncodeFrom<i128> for i8, i16, i32, i64, i128: acc.rs:115-123).  An i128
+ * output is 16 bytes, little-endian two's complement. */
+#define UOR_OUT_I8 1
+#define UOR_OUT_I16 2
+#define UOR_OUT_I32 4
+#define UOR_OUT_I64 8
+#define UOR_OUT_I128 16
+
+/* A strided matrix view over a device buffer: the reference's
+ * MatView::new(data[..len], rows, cols, Strides{rs, cs}) (layout.rs:212) and
+ * MatViewMut::new (layout.rs:384).  `data` is the START of the buffer, not
+ * element (0,0): the view's origin is placed so that the lowest offset it
+ * reaches is element 0, which is how a negative stride walks backwards
+ * through the buffer rather than reading before it. */
+typedef struct uor_view {
+    void *data;
+    uint64_t len; /* buffer length, in elements */
+    uint64_t rows;
+    uint64_t cols;
+    int64_t rs; /* elements between consecutive rows */
+    int64_t cs; /* elements between consecutive columns */
+} uor_view;
+
+/* Which kernels ran: the analogue of the reference's RouteCensus
+ * (crates/uor-matmul-gemm/src/kernel.rs:419-484), which observes the route
+ * without changing it.  May be NULL. */
+#define UOR_ROUTE_NONE 0          /* m == 0 or n == 0: nothing to write */
+#define UOR_ROUTE_EPILOGUE_ONLY 1 /* k == 0: C := enc(beta * C) */
+#define UOR_ROUTE_MFMA_TILE 2     /* int8 MFMA tile, fused epilogue */
+#define UOR_ROUTE_MFMA_SPLITK 3   /* int8 MFMA split-K, exact i64 partials */
+#define UOR_ROUTE_MFMA_WIDE 4     /* int8 MFMA, i64 register widening */
+#define UOR_ROUTE_LUT4_DOT4 10    /* 4-bit table-lookup, LDS codebook */
+#define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
+#define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
+#define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */
+typedef struct uor_route {
+    int32_t kind;
+    int32_t tile_m, tile_n, tile_k;
+    int32_t split_k;
+    int32_t launches;
+    int32_t operand_modes; /* bit 0..1 A load mode, 2..3 B load mode */
+    int32_t moduli;        /* float CRT route: residue moduli used */
+    uint64_t scratch_used; /* bytes of the offer used */
+} uor_route;
+
+/* Returns a static string naming a status code. */
+const char *uor_gfx950_status_string(int status);
+
+/* ===================================================== integer (i8 x i8) */
+
+/*
+ * View API: gemm(&mut Triple, &Linear{alpha,beta}, GemmOptions{encode}, &mut
+ * Scratch) at E = i8 (crates/uor-matmul-gemm/src/kernel.rs:523 gemm_auto,
+ * re-exported as uor_matmul::gemm, crates/uor-matmul/src/lib.rs:135), with
+ * Triple::new's checks (layout.rs:534-575).
+ *
+ *   C := enc(alpha * sum_p A[i,p]*B[p,j] + beta * C[i,j])
+ *
+ * The sum is exact at any depth.  alpha scales it with i128 saturating_mul,
+ * beta*C is added with a wrapping i128 add, and the result is encoded once
+ * (Linear::finish, epilogue.rs:67-95; ScaleExact for i128, epilogue.rs:280-289;
+ * encode_i128_into, acc.rs:128-150).  beta == 0 never reads C (CS-04).
+ * a, b: int8 views; c: a view of `out_type` elements.
+ */
+int uor_gfx950_gemm_i8(const uor_view *a, const uor_view *b, const uor_view *c,
+                       int out_type, int64_t alpha, int64_t beta, int encode,
+                       void *scratch, uint64_t scratch_bytes, void *stream,
+                       uor_route *route);
+
+/*
+ * slice::gemm_ex::<i8, O> (crates/uor-matmul/src/slice.rs:144-178): row-major
+ * with leading dimensions, lengths in elements, encode Nearest.  `scratch` is
+ * a device buffer offer of `scratch_bytes` bytes.
+ */
+int uor_gfx950_slice_gemm_ex_i8(uint64_t m, uint64_t k, uint64_t n, int64_t alpha,
+                                const int8_t *a, uint64_t a_len, uint64_t lda,
+                                const int8_t *b, uint64_t b_len, uint64_t ldb,
+                                int64_t beta, void *c, uint64_t c_len, uint64_t ldc,
+                                int out_type, void *scratch, uint64_t scratch_bytes,
+                                void *stream);
+
+/* slice::gemm::<i8, O> (slice.rs:184-199): gemm_ex(m,k,n,1,a,k,b,n,0,c,n). */
+int uor_gfx950_slice_gemm_i8(uint64_t m, uint64_t k, uint64_t n,
+                             const int8_t *a, uint64_t a_len,
+                             const int8_t *b, uint64_t b_len,
+                             void *c, uint64_t c_len, int out_type,
+                             void *scratch, uint64_t scratch_bytes, void *stream);
+
+/*
+ * The device-route offer that lets every gemm_i8 shape take its fastest route
+ * (split-K partial sums).  Replaces suggested_scratch / suggested_accumulators
+ * (crates/uor-matmul-gemm/src/scratch.rs:183-240) for this backend: the
+ * reference's figure sizes CPU panels, which this route does not use.
+ */
+uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOR_GFX950_H */

@@ -1,0 +1,151 @@
+"""ctypes face of the CPU oracle (oracle/uor_oracle.c) -- TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module. It restates the reference library's semantics on the host so the
+GPU route has something independent to be compared against; the product
+library never calls it.
+
+Views follow the reference's MatView::new (crates/uor-matmul-core/src/layout.rs:212):
+a buffer, a shape and two element strides; the origin is placed so that the
+lowest offset reached is element 0.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
+STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself",
+          3: "short_buffer", 4: "invalid_argument"}
+
+_u64, _i64, _i32, _vp = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+_VIEW = [_vp, _u64, _u64, _u64, _i64, _i64]
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B", "all"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        L.ora_place.argtypes = [_u64, _u64, _u64, _i64, _i64, ctypes.POINTER(_u64)]
+        L.ora_place.restype = _i32
+        L.ora_self_aliases.argtypes = [_u64, _u64, _i64, _i64]
+        L.ora_self_aliases.restype = _i32
+        L.ora_gemm_int.argtypes = [_i32] + _VIEW * 3 + [_i32, _i64, _i64, _i32]
+        L.ora_gemm_int.restype = _i32
+        L.ora_gemm_lut4.argtypes = [_vp, _u64, _u64, _u64, _i64, _i64, _vp, _u64, _u64,
+                                    _vp, _u64, _u64, _vp, _u64, _i64, _i64,
+                                    _i32, _i64, _i64, _i32]
+        L.ora_gemm_lut4.restype = _i32
+        L.ora_gemm_float.argtypes = [_i32] + _VIEW * 3 + [_i64, _i64, _i32]
+        L.ora_gemm_float.restype = _i32
+        L.ora_gemm_trop.argtypes = [_i32] + _VIEW * 3 + [_i32, _i64, _i32, _i64, _i32, _i32]
+        L.ora_gemm_trop.restype = _i32
+        _lib = L
+    return _lib
+
+
+def place(length, rows, cols, rs, cs):
+    """The origin of an rows x cols view in `length` elements, or None."""
+    o = _u64(0)
+    ok = lib().ora_place(length, rows, cols, rs, cs, ctypes.byref(o))
+    return o.value if ok else None
+
+
+def self_aliases(rows, cols, rs, cs) -> bool:
+    return bool(lib().ora_self_aliases(rows, cols, rs, cs))
+
+
+def _ptr(arr):
+    return arr.ctypes.data_as(_vp) if arr.size else None
+
+
+def _view(arr, rows, cols, rs, cs, rec=1):
+    return [_ptr(arr), arr.size // rec, rows, cols, rs, cs]
+
+
+def row_major(rows, cols, ld=None):
+    return (cols if ld is None else ld, 1)
+
+
+_OUT_BYTES = {np.dtype(np.int8): 1, np.dtype(np.int16): 2, np.dtype(np.int32): 4,
+              np.dtype(np.int64): 8}
+
+
+def gemm_int(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+             alpha=1, beta=0, encode="nearest", out_bytes=None):
+    """driver::gemm with Linear{alpha,beta} over ring elements (i8/i16/i32/i64).
+
+    `c` is updated in place; an i128 output is a (len, 2) int64 array / 16-byte
+    records with out_bytes=16. Returns the status name.
+    """
+    eb = a.dtype.itemsize
+    assert b.dtype == a.dtype
+    ob = out_bytes or _OUT_BYTES[c.dtype]
+    rec = 2 if ob == 16 else 1
+    st = lib().ora_gemm_int(eb, *_view(a, *a_shape, *a_strides), *_view(b, *b_shape, *b_strides),
+                            *_view(c, *c_shape, *c_strides, rec=rec), ob, int(alpha), int(beta),
+                            ENCODE[encode])
+    return STATUS[st]
+
+
+def gemm_lut4(a, m, k, a_strides, codes, n, books, group, c, c_strides,
+              alpha=1, beta=0, encode="nearest"):
+    ob = _OUT_BYTES[c.dtype]
+    st = lib().ora_gemm_lut4(_ptr(a), a.size, m, k, *a_strides, _ptr(codes), codes.size, n,
+                             _ptr(books), books.size, group, _ptr(c), c.size, *c_strides,
+                             ob, int(alpha), int(beta), ENCODE[encode])
+    return STATUS[st]
+
+
+def gemm_float(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+               alpha=1, beta=0, encode="nearest"):
+    is64 = a.dtype == np.float64
+    assert b.dtype == a.dtype == c.dtype
+    st = lib().ora_gemm_float(int(is64), *_view(a, *a_shape, *a_strides),
+                              *_view(b, *b_shape, *b_strides), *_view(c, *c_shape, *c_strides),
+                              int(alpha), int(beta), ENCODE[encode])
+    return STATUS[st]
+
+
+def gemm_trop(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+              alpha=(0, True), beta=(0, False), encode="nearest", elem_bytes=1, out_bytes=4):
+    """MaxPlus over Trop records: `a`/`b`/`c` are uint8 byte buffers of
+    2*elem_bytes / 2*out_bytes-byte records. alpha/beta are (value, finite)."""
+    st = lib().ora_gemm_trop(elem_bytes,
+                             *_view(a, *a_shape, *a_strides, rec=2 * elem_bytes),
+                             *_view(b, *b_shape, *b_strides, rec=2 * elem_bytes),
+                             *_view(c, *c_shape, *c_strides, rec=2 * out_bytes),
+                             out_bytes, int(alpha[0]), int(bool(alpha[1])),
+                             int(beta[0]), int(bool(beta[1])), ENCODE[encode])
+    return STATUS[st]
+
+
+# ---------------------------------------------------------------- Trop records
+TROP_I8 = np.dtype([("value", "i1"), ("finite", "u1")])
+TROP_I32 = np.dtype([("value", "<i4"), ("finite", "u1"), ("_pad", "V3")])
+
+
+def trop_i8(values, finite):
+    out = np.zeros(np.shape(values), dtype=TROP_I8)
+    out["value"] = np.where(finite, values, 0)
+    out["finite"] = np.asarray(finite, dtype=np.uint8)
+    return out
+
+
+def trop_bytes(rec):
+    return np.ascontiguousarray(rec).view(np.uint8).reshape(-1)

@@ -1,0 +1,61 @@
+"""The C ABI library: it loads, it exports every function include/uor_gfx950.h
+declares, and its host-side validation (the reference's MatView::new and
+Triple::new, which run before anything is enqueued) answers without a GPU."""
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "uor_gfx950.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(uor_gfx950_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import uor_gfx950
+    lib = uor_gfx950.lib()
+    names = declared()
+    assert names, "the header declares entry points"
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) <= set(uor_gfx950.SYMBOLS) | set(names)
+
+
+def test_status_strings():
+    import uor_gfx950
+    lib = uor_gfx950.lib()
+    assert lib.uor_gfx950_status_string(0) == b"ok"
+    assert lib.uor_gfx950_status_string(1) == b"nonconformant"
+    assert lib.uor_gfx950_status_string(2) == b"output_aliases_itself"
+    assert lib.uor_gfx950_status_string(3) == b"short_buffer"
+
+
+def _v(ptr, length, rows, cols, rs, cs):
+    import uor_gfx950
+    return uor_gfx950.View(ptr, length, rows, cols, rs, cs)
+
+
+def test_validation_statuses_without_a_gpu():
+    """Non-existence is reported before any device work (error.rs:28-53).
+    Fake non-null addresses are never dereferenced: every request here fails
+    validation."""
+    import uor_gfx950
+    lib = uor_gfx950.lib()
+    P = 0x1000
+    call = lambda a, b, c, ob=4, enc=0: lib.uor_gfx950_gemm_i8(
+        ctypes.byref(a), ctypes.byref(b), ctypes.byref(c), ob, 1, 0, enc, None, 0, None, None)
+    assert call(_v(P, 12, 3, 4, 4, 1), _v(P, 12, 3, 4, 4, 1), _v(P, 16, 3, 4, 4, 1)) == 1
+    assert call(_v(P, 12, 3, 4, 4, 1), _v(P, 12, 4, 3, 3, 1), _v(P, 9, 3, 4, 4, 1)) == 3
+    assert call(_v(P, 12, 3, 4, 4, 1), _v(P, 12, 4, 3, 3, 1), _v(P, 9, 3, 3, 1, 1)) == 2
+    assert call(_v(P, 12, 3, 4, 4, 1), _v(P, 12, 4, 3, 3, 1), _v(P, 9, 3, 3, 3, 1), ob=3) == 4
+    assert call(_v(P, 12, 3, 4, 4, 1), _v(P, 12, 4, 3, 3, 1), _v(P, 9, 3, 3, 3, 1), enc=7) == 4
+    # 5 x 1 at rs = 1 << 62: the reach overflows, so no such view exists.
+    assert call(_v(P, 100, 5, 1, 1 << 62, 1), _v(P, 1, 1, 1, 1, 1), _v(P, 5, 5, 1, 1, 1)) == 3
+    # The slice face: a short slice is status 3 (does_not_fit, slice.rs:104-116).
+    assert lib.uor_gfx950_slice_gemm_i8(4, 4, 4, P, 15, P, 16, P, 16, 4, None, 0, None) == 3

@@ -1,0 +1,266 @@
+"""GPU parity of the exact i8 GEMM route (through the C ABI) against the oracle.
+
+Bar: bit-exact.  Small and ragged cases compare with the CPU oracle
+(oracle/uor_oracle.c); the full-size configurations compare with float64
+matmul, which is exact here because every partial sum is an integer below
+2^53, plus oracle rows and closed forms for the deep case.
+"""
+import numpy as np
+import pytest
+import torch
+
+import gen
+
+pytestmark = pytest.mark.gpu
+
+I32_MAX = (1 << 31) - 1
+
+
+def to_dev(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def dev_i8(x, dev):
+    return to_dev(np.asarray(x, dtype=np.int8), dev)
+
+
+def check_case(oracle, uor, dev, a, ash, ast, b, bsh, bst, c0, csh, cst, out="i32", alpha=1,
+               beta=0, encode="nearest", scratch=None, expect_route=None):
+    dt = {"i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64}[out]
+    want = c0.copy()
+    st = oracle.gemm_int(a, ash, ast, b, bsh, bst, want, csh, cst, alpha=alpha, beta=beta,
+                         encode=encode)
+    ga, gb, gc = to_dev(a, dev), to_dev(b, dev), to_dev(c0, dev)
+    gst, route = uor.gemm_i8(ga, ash, ast, gb, bsh, bst, gc, csh, cst, out=out, alpha=alpha,
+                             beta=beta, encode=encode, scratch=scratch)
+    torch.cuda.synchronize()
+    assert uor.STATUS.get(gst, gst) == st
+    got = gc.cpu().numpy()
+    assert got.dtype == dt
+    assert np.array_equal(got, want), (ash, bsh, csh, out, alpha, beta, encode, route)
+    if expect_route:
+        assert route["kind"] == expect_route, route
+    return route
+
+
+def test_readme_and_cs05_cs06(oracle, uor, dev):
+    a = np.array([1, 2, 3, 4], np.int8)
+    b = np.array([5, 6, 7, 8], np.int8)
+    c = torch.zeros(4, dtype=torch.int32, device=dev)
+    assert uor.slice_gemm_i8(2, 2, 2, dev_i8(a, dev), dev_i8(b, dev), c) == 0
+    torch.cuda.synchronize()
+    assert c.cpu().tolist() == [19, 22, 43, 50]
+    c = torch.tensor([100, 200, 300, 400], dtype=torch.int32, device=dev)
+    assert uor.slice_gemm_ex_i8(2, 2, 2, 3, dev_i8(a, dev), 2, dev_i8(b, dev), 2, -2, c, 2) == 0
+    torch.cuda.synchronize()
+    assert c.cpu().tolist() == [3 * 19 - 200, 3 * 22 - 400, 3 * 43 - 600, 3 * 50 - 800]
+    a6 = np.array([1, 2, 3, 4, 5, 6], np.int8)
+    d = np.zeros(9, np.int32)
+    check_case(oracle, uor, dev, a6, (3, 2), (1, 3), a6, (2, 3), (3, 1), d, (3, 3), (3, 1))
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (13, 17, 19), (64, 64, 64), (65, 130, 67),
+                                   (127, 255, 129), (200, 1000, 300), (31, 4099, 33)])
+@pytest.mark.parametrize("layout", ["nn", "tn", "nt", "tt"])
+def test_layouts_against_oracle(oracle, uor, dev, shape, layout):
+    m, k, n = shape
+    rng = np.random.default_rng(m * 7919 + k * 31 + n)
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    ast = (k, 1) if layout[0] == "n" else (1, m)
+    bst = (n, 1) if layout[1] == "n" else (1, k)
+    c0 = np.zeros(m * n, np.int32)
+    check_case(oracle, uor, dev, a, (m, k), ast, b, (k, n), bst, c0, (m, n), (n, 1))
+
+
+@pytest.mark.parametrize("out", ["i8", "i16", "i32", "i64"])
+@pytest.mark.parametrize("encode", ["nearest", "saturating", "toward_zero", "wrapping"])
+def test_output_types_and_encodes(oracle, uor, dev, out, encode):
+    dt = {"i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64}[out]
+    rng = np.random.default_rng(hash((out, encode)) & 0xFFFF)
+    m, k, n = 37, 300, 41
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    c0 = rng.integers(np.iinfo(dt).min, np.iinfo(dt).max, m * n, dtype=dt, endpoint=True)
+    for alpha, beta in [(1, 0), (3, -1), (-(1 << 40), 1 << 33), (1 << 62, -(1 << 62)),
+                        (-(1 << 63), (1 << 63) - 1)]:
+        check_case(oracle, uor, dev, a, (m, k), (k, 1), b, (k, n), (n, 1), c0, (m, n), (n, 1),
+                   out=out, alpha=alpha, beta=beta, encode=encode)
+
+
+def test_i128_output(oracle, uor, dev):
+    rng = np.random.default_rng(5)
+    m, k, n = 9, 70, 11
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    c0 = rng.integers(-(1 << 62), 1 << 62, 2 * m * n, dtype=np.int64)
+    for alpha, beta, enc in [(1, 0, "nearest"), (5, -7, "wrapping"),
+                             ((1 << 63) - 1, -(1 << 63), "saturating")]:
+        want = c0.copy()
+        assert oracle.gemm_int(a, (m, k), (k, 1), b, (k, n), (n, 1), want, (m, n), (n, 1),
+                               alpha=alpha, beta=beta, encode=enc, out_bytes=16) == "ok"
+        gc = to_dev(c0, dev)
+        st, _ = uor.gemm_i8(to_dev(a, dev), (m, k), (k, 1), to_dev(b, dev), (k, n), (n, 1), gc,
+                            (m, n), (n, 1), out="i128", alpha=alpha, beta=beta, encode=enc)
+        torch.cuda.synchronize()
+        assert st == 0 and np.array_equal(gc.cpu().numpy(), want), (alpha, beta, enc)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_strided_views(oracle, uor, dev, seed):
+    """Negative, zero, transposed and misaligned strides (the view API's
+    arbitrary strides, layout.rs:29-154) go through the gathering loaders."""
+    rng = np.random.default_rng(100 + seed)
+    for _ in range(12):
+        m, k, n = (int(x) for x in rng.integers(1, 70, 3))
+        def pick(rows, cols):
+            choice = rng.integers(0, 5)
+            if choice == 0:
+                return cols, 1
+            if choice == 1:
+                return 1, rows
+            if choice == 2:
+                return -cols, 1
+            if choice == 3:
+                return 0, 1
+            return int(rng.integers(-3, 4)) * cols + 1, int(rng.choice([-1, 1, 2]))
+        ars, acs = pick(m, k)
+        brs, bcs = pick(k, n)
+        a = rng.integers(-128, 128, 4 * (m * k + 1) + 64).astype(np.int8)
+        b = rng.integers(-128, 128, 4 * (k * n + 1) + 64).astype(np.int8)
+        if oracle.place(a.size, m, k, ars, acs) is None or oracle.place(b.size, k, n, brs, bcs) is None:
+            continue
+        c0 = rng.integers(-1000, 1000, m * n).astype(np.int32)
+        crs, ccs = (n, 1) if rng.random() < 0.5 else (1, m)
+        check_case(oracle, uor, dev, a, (m, k), (ars, acs), b, (k, n), (brs, bcs), c0, (m, n),
+                   (crs, ccs), alpha=int(rng.integers(-4, 5)), beta=int(rng.integers(-4, 5)))
+
+
+def test_misaligned_and_offset_buffers(oracle, uor, dev):
+    rng = np.random.default_rng(9)
+    m, k, n = 100, 150, 90
+    a_full = rng.integers(-128, 128, m * k + 3).astype(np.int8)
+    b_full = rng.integers(-128, 128, k * n + 5).astype(np.int8)
+    ga, gb = to_dev(a_full, dev), to_dev(b_full, dev)
+    gc = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    st, route = uor.gemm_i8(ga[3:], (m, k), (k, 1), gb[5:], (k, n), (n, 1), gc, (m, n), (n, 1))
+    torch.cuda.synchronize()
+    want = np.zeros(m * n, np.int32)
+    oracle.gemm_int(a_full[3:].copy(), (m, k), (k, 1), b_full[5:].copy(), (k, n), (n, 1), want,
+                    (m, n), (n, 1))
+    assert st == 0 and np.array_equal(gc.cpu().numpy(), want)
+    assert route["operand_modes"] == 2 | (2 << 2)  # both gathered
+
+
+def test_empty_and_k_zero(oracle, uor, dev):
+    c0 = np.arange(12, dtype=np.int32)
+    r = check_case(oracle, uor, dev, np.zeros(0, np.int8), (3, 0), (0, 1),
+                   np.zeros(0, np.int8), (0, 4), (4, 1), c0, (3, 4), (4, 1), alpha=5, beta=-3)
+    assert r["kind"] == "epilogue_only"
+    r = check_case(oracle, uor, dev, np.zeros(0, np.int8), (0, 5), (5, 1),
+                   np.zeros(35, np.int8), (5, 7), (7, 1), np.zeros(0, np.int32), (0, 7), (7, 1))
+    assert r["kind"] == "none"
+
+
+def test_errors_report_before_launch(uor, dev):
+    a = torch.zeros(12, dtype=torch.int8, device=dev)
+    c = torch.zeros(16, dtype=torch.int32, device=dev)
+    assert uor.gemm_i8(a, (3, 4), (4, 1), a, (3, 4), (4, 1), c, (3, 4), (4, 1))[0] == 1
+    assert uor.gemm_i8(a, (3, 4), (4, 1), a, (4, 3), (3, 1), c, (3, 3), (1, 1))[0] == 2
+    assert uor.gemm_i8(a, (3, 5), (5, 1), a, (5, 3), (3, 1), c, (3, 3), (3, 1))[0] == 3
+
+
+def test_offer_ladder_same_bytes_cd10(oracle, uor, dev):
+    """Every scratch offer, from none to suggested, gives identical bytes;
+    only the route changes (reference CD-10, CD-22)."""
+    rng = np.random.default_rng(77)
+    m, k, n = 96, 140_000, 80
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    ga, gb = to_dev(a, dev), to_dev(b, dev)
+    want = (a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64))
+    want = np.clip(3 * want - 7, -(1 << 31), I32_MAX).astype(np.int32)
+    kinds = set()
+    for offer in [0, 100, uor.suggested_scratch_i8(m, k, n)]:
+        scratch = torch.empty(max(offer, 1), dtype=torch.uint8, device=dev) if offer else None
+        gc = torch.ones(m * n, dtype=torch.int32, device=dev) * 7
+        st, route = uor.gemm_i8(ga, (m, k), (k, 1), gb, (k, n), (n, 1), gc, (m, n), (n, 1),
+                                alpha=3, beta=-1, scratch=scratch)
+        torch.cuda.synchronize()
+        assert st == 0
+        assert np.array_equal(gc.cpu().numpy().reshape(m, n), want), route
+        kinds.add(route["kind"])
+    assert kinds == {"mfma_wide", "mfma_splitk"}
+
+
+def test_config1_slice_gemm_1024(uor, dev):
+    """slice::gemm i8 -> i32, 1024^3, xorshift fill (salts 1, 2),
+    suggested scratch offer; the reference's exact generator sequence."""
+    n = 1024
+    a = gen.i8_full(n * n, 1, exact_sequence=True)
+    b = gen.i8_full(n * n, 2, exact_sequence=True)
+    want = (a.reshape(n, n).astype(np.float64) @ b.reshape(n, n).astype(np.float64)).astype(np.int32)
+    scratch = torch.empty(uor.suggested_scratch_i8(n, n, n), dtype=torch.uint8, device=dev)
+    gc = torch.full((n * n,), 0x7B7B7B7B, dtype=torch.int32, device=dev)
+    assert uor.slice_gemm_i8(n, n, n, to_dev(a, dev), to_dev(b, dev), gc, scratch=scratch) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(gc.cpu().numpy().reshape(n, n), want)
+
+
+def test_config2_gemm_ex_8192_padded(oracle, uor, dev):
+    """gemm_ex 8192^3, lda=ldb=ldc=8256, alpha=3, beta=-1, C
+    uniform in [-2^20, 2^20]; padding columns must be neither read into the
+    result nor written."""
+    N, LD = 8192, 8256
+    a = gen.i8_full(N * LD, 3)
+    b = gen.i8_full(N * LD, 4)
+    c0 = gen.i32_pm2_20(N * LD, 5)
+    ga, gb, gc = to_dev(a, dev), to_dev(b, dev), to_dev(c0, dev)
+    pad_before = gc.view(N, LD)[:, N:].clone()
+    assert uor.slice_gemm_ex_i8(N, N, N, 3, ga, LD, gb, LD, -1, gc, LD) == 0
+    torch.cuda.synchronize()
+    A = ga.view(N, LD)[:, :N].to(torch.float64)
+    B = gb.view(N, LD)[:, :N].to(torch.float64)
+    C0 = to_dev(c0, dev).view(N, LD)[:, :N].to(torch.float64)
+    want = 3 * (A @ B) - C0  # exact: |values| < 2^30
+    got = gc.view(N, LD)[:, :N].to(torch.float64)
+    assert torch.equal(got, want)
+    assert torch.equal(gc.view(N, LD)[:, N:], pad_before)
+    del A, B, C0, want, got
+    # Rows against the oracle itself.
+    rows = [0, 1, 4095, 8191]
+    for r in rows:
+        ar = a.reshape(N, LD)[r, :N].copy()
+        c = c0.reshape(N, LD)[r, :N].copy()
+        oracle.gemm_int(ar, (1, N), (N, 1), b, (N, N), (LD, 1), c, (1, N), (N, 1), alpha=3, beta=-1)
+        assert np.array_equal(gc.view(N, LD)[r, :N].cpu().numpy(), c), r
+
+
+@pytest.mark.parametrize("out,alpha,beta,encode", [
+    ("i32", 1, 0, "nearest"), ("i64", 1, 0, "nearest"), ("i64", 3, -1, "nearest"),
+    ("i32", 1, 0, "wrapping"), ("i32", 3, -1, "nearest")])
+def test_config2_deep_k_2_24(uor, dev, out, alpha, beta, encode):
+    """configs[1] deep case: m=n=128, k=2^24, A=B=-128, so every exact sum is
+    2^38: i32 Nearest saturates to i32::MAX, i64 holds 2^38 (or 3*2^38 - C),
+    Wrapping gives 2^38 mod 2^32 = 0."""
+    m = n = 128
+    k = 1 << 24
+    ga = torch.full((m * k,), -128, dtype=torch.int8, device=dev)
+    gb = torch.full((k * n,), -128, dtype=torch.int8, device=dev)
+    dt = torch.int32 if out == "i32" else torch.int64
+    c0 = torch.arange(m * n, dtype=dt, device=dev) - 5000
+    gc = c0.clone()
+    scratch = torch.empty(uor.suggested_scratch_i8(m, k, n), dtype=torch.uint8, device=dev)
+    st, route = uor.gemm_i8(ga, (m, k), (k, 1), gb, (k, n), (n, 1), gc, (m, n), (n, 1), out=out,
+                            alpha=alpha, beta=beta, encode=encode, scratch=scratch)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_splitk"
+    exact = alpha * (1 << 38)
+    want = [exact + beta * int(v) for v in c0.cpu().tolist()]
+    bits = 32 if out == "i32" else 64
+    mn, mx = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+    if encode == "wrapping":
+        want = [(v - mn) % (1 << bits) + mn for v in want]
+    else:
+        want = [max(mn, min(mx, v)) for v in want]
+    assert gc.cpu().tolist() == want

@@ -1,0 +1,173 @@
+"""Pins the integer oracle (driver::gemm + Linear + encode) independently.
+
+Witnesses: the reference's committed CX-10 fixtures (oracles/numpy: NumPy int64
+matmul, Wrapping, sha256-checked), NumPy int64 matmul over i8 (exact), Python
+integers for the encode rules, and the reference's inline known answers.
+"""
+import hashlib
+import json
+
+import numpy as np
+import pytest
+from numpy.lib.stride_tricks import as_strided
+
+from conftest import GOLDEN
+
+I32_MIN, I32_MAX = -(1 << 31), (1 << 31) - 1
+
+
+def run(oracle, a, am, ak, ars, acs, b, bk, bn, brs, bcs, c, crs, ccs, **kw):
+    st = oracle.gemm_int(a, (am, ak), (ars, acs), b, (bk, bn), (brs, bcs), c, (am, bn),
+                         (crs, ccs), **kw)
+    return st
+
+
+def test_readme_example(oracle):
+    a = np.array([1, 2, 3, 4], np.int8)
+    b = np.array([5, 6, 7, 8], np.int8)
+    c = np.zeros(4, np.int32)
+    assert run(oracle, a, 2, 2, 2, 1, b, 2, 2, 2, 1, c, 2, 1) == "ok"
+    assert c.tolist() == [19, 22, 43, 50]  # README.md:38-39
+
+
+def test_alpha_beta_cs05(oracle):
+    a = np.array([1, 2, 3, 4], np.int8)
+    b = np.array([5, 6, 7, 8], np.int8)
+    c = np.array([100, 200, 300, 400], np.int32)
+    run(oracle, a, 2, 2, 2, 1, b, 2, 2, 2, 1, c, 2, 1, alpha=3, beta=-2)
+    assert c.tolist() == [3 * 19 - 200, 3 * 22 - 400, 3 * 43 - 600, 3 * 50 - 800]
+
+
+def test_transposed_strides_cs06(oracle):
+    a = np.array([1, 2, 3, 4, 5, 6], np.int8)
+    b = np.array([1, 2, 3, 4, 5, 6], np.int8)
+    c = np.zeros(4, np.int32)
+    run(oracle, a, 2, 3, 3, 1, b, 3, 2, 2, 1, c, 2, 1)
+    assert c.tolist() == [22, 28, 49, 64]
+    d = np.zeros(9, np.int32)
+    run(oracle, a, 3, 2, 1, 3, b, 2, 3, 3, 1, d, 3, 1)
+    assert d.tolist() == [17, 22, 27, 22, 29, 36, 27, 36, 45]
+
+
+def test_encode_modes_cd05(oracle):
+    # kernel.rs:2315-2386: 500*127^2 fits; 200000*127^2 wraps vs saturates.
+    a = np.full(4 * 500, 127, np.int8)
+    c = np.zeros(16, np.int32)
+    run(oracle, a, 4, 500, 500, 1, a, 500, 4, 4, 1, c, 4, 1, encode="wrapping")
+    assert c[0] == 500 * 127 * 127
+    deep = 200_000
+    a = np.full(deep, 127, np.int8)
+    w = np.zeros(1, np.int32)
+    s = np.zeros(1, np.int32)
+    run(oracle, a, 1, deep, deep, 1, a, deep, 1, 1, 1, w, 1, 1, encode="wrapping")
+    run(oracle, a, 1, deep, deep, 1, a, deep, 1, 1, 1, s, 1, 1, encode="saturating")
+    assert w[0] == np.int64(deep * 127 * 127).astype(np.int32)
+    assert s[0] == I32_MAX
+
+
+@pytest.mark.parametrize("k", [150_000, 300_000])
+def test_depth_past_every_lane_ct01(oracle, k):
+    a = np.full(k, -128, np.int8)
+    c64 = np.zeros(1, np.int64)
+    run(oracle, a, 1, k, k, 1, a, k, 1, 1, 1, c64, 1, 1)
+    assert c64[0] == k * 128 * 128
+    c32 = np.zeros(1, np.int32)
+    run(oracle, a, 1, k, k, 1, a, k, 1, 1, 1, c32, 1, 1, encode="wrapping")
+    assert c32[0] == np.int64(k * 128 * 128).astype(np.int32)
+
+
+def test_numpy_cx10_fixtures(oracle):
+    d = GOLDEN / "numpy_cx10"
+    man = json.loads((d / "manifest.json").read_text())
+    assert man["id"] == "CX-10" and man["dtype"] == "int64"
+    for case in man["cases"]:
+        m, k, n = (case["shape"][x] for x in "mkn")
+        blobs = {}
+        for name in ("a", "b", "expected"):
+            raw = (d / f"{case['stem']}.{name}.bin").read_bytes()
+            assert "sha256:" + hashlib.sha256(raw).hexdigest() == case[f"{name}_sha256" if name != "expected" else "expected_sha256"]
+            blobs[name] = np.frombuffer(raw, "<i8").copy()
+        c = np.zeros(m * n, np.int64)
+        if m and n:
+            st = oracle.gemm_int(blobs["a"], (m, k), (k, 1), blobs["b"], (k, n), (n, 1), c,
+                                 (m, n), (n, 1), encode="wrapping")
+            assert st == "ok"
+        assert np.array_equal(c, blobs["expected"]), case["stem"]
+
+
+def strided(buf, rows, cols, rs, cs, origin):
+    item = buf.itemsize
+    return as_strided(buf[origin:], shape=(rows, cols), strides=(rs * item, cs * item))
+
+
+def encode_py(v, bits, mode):
+    mn, mx = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+    if mode == "wrapping":
+        return (v - mn) % (1 << bits) + mn
+    return max(mn, min(mx, v))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_views_match_numpy(oracle, seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(25):
+        m, k, n = (int(x) for x in rng.integers(0, 9, 3))
+        def pick(rows, cols):
+            rs = int(rng.choice([-1, 1])) * int(rng.integers(0, 3)) * max(cols, 1)
+            cs = int(rng.choice([-1, 1])) * int(rng.integers(0, 2))
+            if rng.random() < 0.3:
+                rs, cs = cs, rs
+            return rs, cs
+        ars, acs = pick(m, k)
+        brs, bcs = pick(k, n)
+        a = rng.integers(-128, 128, size=3 * (m * k + 1) + 30).astype(np.int8)
+        b = rng.integers(-128, 128, size=3 * (k * n + 1) + 30).astype(np.int8)
+        ao = oracle.place(a.size, m, k, ars, acs)
+        bo = oracle.place(b.size, k, n, brs, bcs)
+        if ao is None or bo is None:
+            continue
+        c = rng.integers(-1000, 1000, size=m * n).astype(np.int32)
+        alpha, beta = int(rng.integers(-5, 6)), int(rng.integers(-5, 6))
+        A = strided(a, m, k, ars, acs, ao).astype(np.int64) if m and k else np.zeros((m, k), np.int64)
+        B = strided(b, k, n, brs, bcs, bo).astype(np.int64) if k and n else np.zeros((k, n), np.int64)
+        want = alpha * (A @ B) + (beta * c.reshape(m, n).astype(np.int64) if beta else 0)
+        st = oracle.gemm_int(a, (m, k), (ars, acs), b, (k, n), (brs, bcs), c, (m, n), (n, 1),
+                             alpha=alpha, beta=beta)
+        assert st == "ok"
+        assert np.array_equal(c.reshape(m, n), np.vectorize(lambda v: encode_py(int(v), 32, "nearest"))(want).astype(np.int32) if m and n else c.reshape(m, n))
+
+
+@pytest.mark.parametrize("out,bits", [(np.int8, 8), (np.int16, 16), (np.int32, 32), (np.int64, 64)])
+@pytest.mark.parametrize("mode", ["nearest", "saturating", "toward_zero", "wrapping"])
+def test_encode_rules_against_python_ints(oracle, out, bits, mode):
+    rng = np.random.default_rng(bits)
+    m, k, n = 5, 300, 6
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    c0 = rng.integers(np.iinfo(out).min, np.iinfo(out).max, m * n, dtype=out, endpoint=True)
+    for alpha, beta in [(1, 0), (7, -3), (-(1 << 40), 1 << 33), (1 << 62, -(1 << 62))]:
+        c = c0.copy()
+        assert oracle.gemm_int(a, (m, k), (k, 1), b, (k, n), (n, 1), c, (m, n), (n, 1),
+                               alpha=alpha, beta=beta, encode=mode) == "ok"
+        S = a.reshape(m, k).astype(object) @ b.reshape(k, n).astype(object)
+        for idx in range(m * n):
+            v = alpha * int(S.flat[idx]) + (beta * int(c0[idx]) if beta else 0)
+            assert int(c[idx]) == encode_py(v, bits, mode), (alpha, beta, idx)
+
+
+def test_beta_zero_never_reads_c(oracle):
+    rng = np.random.default_rng(1)
+    a = rng.integers(-128, 128, 12).astype(np.int8)
+    c1 = np.full(9, 0x5A5A5A5A, np.int32)
+    c2 = np.full(9, -1, np.int32)
+    for c in (c1, c2):
+        oracle.gemm_int(a, (3, 4), (4, 1), a, (4, 3), (3, 1), c, (3, 3), (3, 1), alpha=2, beta=0)
+    assert np.array_equal(c1, c2)
+
+
+def test_errors(oracle):
+    a = np.zeros(12, np.int8)
+    c = np.zeros(16, np.int32)
+    assert oracle.gemm_int(a, (3, 4), (4, 1), a, (3, 4), (4, 1), c, (3, 4), (4, 1)) == "nonconformant"
+    assert oracle.gemm_int(a, (3, 4), (4, 1), a, (4, 3), (3, 1), c, (3, 3), (1, 1)) == "output_aliases_itself"
+    assert oracle.gemm_int(a, (3, 5), (5, 1), a, (5, 3), (3, 1), c, (3, 3), (3, 1)) == "short_buffer"

@@ -1,0 +1,626 @@
+// Exact i8 x i8 GEMM on gfx950 int8 MFMA.
+//
+// Replaces the reference's packed auto route for i8 (gemm_auto ->
+// gemm_packed_impl -> run, crates/uor-matmul-gemm/src/kernel.rs:523-1377, with
+// the KernelSpec::mac_tile sequences of crates/uor-matmul-kernels/src/isa/
+// x86.rs:80-96, 704-897) at the whole-product level.
+//
+// Exactness: each v_mfma_i32_32x32x32_i8 accumulates into i32.  A product of
+// two i8 has magnitude <= 2^14, so an i32 lane holds any sum of at most
+// KCHUNK = 65536 terms exactly (2^30 < 2^31) -- the reference's lane_depth
+// argument (crates/uor-matmul-kernels/src/spec.rs:232-243).  Deeper sums are
+// widened into i64 exactly: per-KCHUNK segments are added into i64 registers
+// (WIDE) or into an i64 partial-sum workspace with integer atomics (SPLITK),
+// which is order-independent, so the bytes never depend on the schedule
+// (reference CD-02).  |sum| < 2^63 for every k a device can reach
+// (k < 2^49), so i64 holds the exact value the reference keeps in i128.
+//
+// Data layout in LDS, per operand and pipeline stage: the tile's BK bytes of
+// reduction are split in 16-byte chunks; chunk c of tile row r (an m row for
+// A, an n column for B) sits at c*CSTRIDE + 16*r + 16*(r/16).  Each MFMA lane
+// reads one 16-byte chunk with ds_read_b128; the 16-byte gap every 16 rows and
+// the chunk-stride pad keep the 64 lanes on distinct banks for both the
+// fragment reads and the transposing dword writes.
+
+#include "common.hpp"
+
+namespace uor {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int KCHUNK = 65536;
+constexpr int NTHREADS = 256;
+
+// How an operand tile reaches LDS.
+enum : int {
+    LOAD_K = 0,   // reduction axis contiguous (row-major A, column-major B): 16B loads
+    LOAD_MN = 1,  // m/n axis contiguous (column-major A, row-major B): 16B loads + 4x4 byte transpose
+    LOAD_GEN = 2  // any strides, including negative and zero: byte gathers
+};
+
+enum : int { EPI_FUSED = 0, EPI_PARTIAL = 1, EPI_WIDE = 2 };
+
+// A placed operand seen from the reduction: element (mn, p) is at
+// base + mn*s_mn + p*s_k.
+struct Opnd {
+    const int8_t *base;
+    int64_t s_mn, s_k;
+    uint64_t mn;  // extent along m (A) or n (B)
+};
+
+struct OutArgs {
+    char *base;  // element (0,0) of C
+    int64_t rs, cs;  // in elements
+    int ob;          // output bytes
+    int64_t alpha, beta;
+    int mode;
+    long long *work;  // SPLITK: m x n exact partial sums, row-major
+};
+
+template <int BMN, int BK>
+struct Layout {
+    static constexpr int CHUNKS = BK / 16;
+    static constexpr int CSTRIDE = BMN * 16 + (BMN / 16) * 16 + 64;
+    static constexpr int BYTES = CHUNKS * CSTRIDE;
+    __device__ static inline int off(int c, int r) { return c * CSTRIDE + r * 16 + (r >> 4) * 16; }
+};
+
+// ---------------------------------------------------------------- loaders --
+
+// Sixteen bytes p[0], p[step], ..., p[15*step], each only if its index is
+// below `valid`; missing bytes read as zero.  Fully unrolled so the result
+// stays in registers.
+__device__ inline v4i gather16(const int8_t *p, int64_t step, uint64_t valid) {
+    uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        uint32_t x = (uint64_t)b < valid ? (uint32_t)(uint8_t)p[(int64_t)b * step] : 0u;
+        x <<= 8 * (b & 3);
+        if (b < 4) w0 |= x;
+        else if (b < 8) w1 |= x;
+        else if (b < 12) w2 |= x;
+        else w3 |= x;
+    }
+    return v4i{(int)w0, (int)w1, (int)w2, (int)w3};
+}
+
+template <int MODE, int BMN, int BK>
+struct Loader;
+
+// Reduction axis contiguous: chunk q of the tile is row q/CHUNKS, chunk q%CHUNKS.
+template <int BMN, int BK>
+struct Loader<LOAD_K, BMN, BK> {
+    static constexpr int CHUNKS = BK / 16;
+    static constexpr int PER = (BMN * CHUNKS + NTHREADS - 1) / NTHREADS;
+    v4i r[PER];
+
+    __device__ inline void load(const Opnd &o, uint64_t mn0, uint64_t k0, uint64_t K) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + NTHREADS * i;
+            int row = q / CHUNKS, c = q % CHUNKS;
+            uint64_t mn = mn0 + row, k = k0 + 16 * c;
+            v4i v = {0, 0, 0, 0};
+            if (q < BMN * CHUNKS && mn < o.mn && k < K) {
+                const int8_t *p = o.base + (int64_t)mn * o.s_mn + (int64_t)k;
+                if (k + 16 <= K) v = *(const v4i *)p;
+                else v = gather16(p, 1, K - k);
+            }
+            r[i] = v;
+        }
+    }
+    __device__ inline void store(char *lds) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + NTHREADS * i;
+            if (q < BMN * CHUNKS)
+                *(v4i *)(lds + Layout<BMN, BK>::off(q % CHUNKS, q / CHUNKS)) = r[i];
+        }
+    }
+};
+
+// Any strides: the same chunk assignment as LOAD_K, gathered byte by byte.
+template <int BMN, int BK>
+struct Loader<LOAD_GEN, BMN, BK> {
+    static constexpr int CHUNKS = BK / 16;
+    static constexpr int PER = (BMN * CHUNKS + NTHREADS - 1) / NTHREADS;
+    v4i r[PER];
+
+    __device__ inline void load(const Opnd &o, uint64_t mn0, uint64_t k0, uint64_t K) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + NTHREADS * i;
+            int row = q / CHUNKS, c = q % CHUNKS;
+            uint64_t mn = mn0 + row, k = k0 + 16 * c;
+            v4i v = {0, 0, 0, 0};
+            if (q < BMN * CHUNKS && mn < o.mn && k < K)
+                v = gather16(o.base + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k, o.s_k, K - k);
+            r[i] = v;
+        }
+    }
+    __device__ inline void store(char *lds) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + NTHREADS * i;
+            if (q < BMN * CHUNKS)
+                *(v4i *)(lds + Layout<BMN, BK>::off(q % CHUNKS, q / CHUNKS)) = r[i];
+        }
+    }
+};
+
+// m/n axis contiguous: a thread loads a 4 (reduction) x 16 (m/n) byte block
+// as four 16-byte rows and transposes it into sixteen dwords, each holding
+// four consecutive reduction positions of one m/n index.
+template <int BMN, int BK>
+struct Loader<LOAD_MN, BMN, BK> {
+    static constexpr int MB = BMN / 16;           // 16-wide m/n blocks
+    static constexpr int BLOCKS = MB * (BK / 4);  // 4-deep reduction blocks
+    static constexpr int PER = (BLOCKS + NTHREADS - 1) / NTHREADS;
+    v4i r[PER][4];
+
+    __device__ inline void load(const Opnd &o, uint64_t mn0, uint64_t k0, uint64_t K) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + NTHREADS * i;
+            int mb = q % MB, kb = q / MB;
+            uint64_t mn = mn0 + 16 * mb;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint64_t k = k0 + 4 * kb + t;
+                v4i v = {0, 0, 0, 0};
+                if (q < BLOCKS && k < K && mn < o.mn) {
+                    const int8_t *p = o.base + (int64_t)k * o.s_k + (int64_t)mn;
+                    if (mn + 16 <= o.mn) v = *(const v4i *)p;
+                    else v = gather16(p, 1, o.mn - mn);
+                }
+                r[i][t] = v;
+            }
+        }
+    }
+    __device__ inline void store(char *lds) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + NTHREADS * i;
+            if (q >= BLOCKS) continue;
+            int mb = q % MB, kb = q / MB;
+            int c = kb >> 2, sub = 4 * (kb & 3);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t r0 = r[i][0][d], r1 = r[i][1][d], r2 = r[i][2][d], r3 = r[i][3][d];
+                uint32_t lo01 = __builtin_amdgcn_perm(r1, r0, 0x05010400u);
+                uint32_t hi01 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);
+                uint32_t lo23 = __builtin_amdgcn_perm(r3, r2, 0x05010400u);
+                uint32_t hi23 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+                uint32_t e0 = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+                uint32_t e1 = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+                uint32_t e2 = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+                uint32_t e3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+                int row = 16 * mb + 4 * d;
+                *(uint32_t *)(lds + Layout<BMN, BK>::off(c, row + 0) + sub) = e0;
+                *(uint32_t *)(lds + Layout<BMN, BK>::off(c, row + 1) + sub) = e1;
+                *(uint32_t *)(lds + Layout<BMN, BK>::off(c, row + 2) + sub) = e2;
+                *(uint32_t *)(lds + Layout<BMN, BK>::off(c, row + 3) + sub) = e3;
+            }
+        }
+    }
+};
+
+// -------------------------------------------------------------- epilogue --
+
+template <bool FAST>
+__device__ inline void finish_any(const OutArgs &o, char *cp, int64_t sum) {
+    switch (o.ob) {
+    case 1: linear_finish<1, FAST>(cp, sum, o.alpha, o.beta, o.mode); break;
+    case 2: linear_finish<2, FAST>(cp, sum, o.alpha, o.beta, o.mode); break;
+    case 4: linear_finish<4, FAST>(cp, sum, o.alpha, o.beta, o.mode); break;
+    case 8: linear_finish<8, FAST>(cp, sum, o.alpha, o.beta, o.mode); break;
+    default: linear_finish<16, false>(cp, sum, o.alpha, o.beta, o.mode); break;
+    }
+}
+
+// Tile index -> (tile row, tile column).  Workgroups are dealt round-robin to
+// the 8 XCDs, so consecutive ids are remapped onto one XCD first, then walked
+// in groups of 8 tile rows so that the tiles one XCD holds at a time share
+// A rows and B columns in its L2.
+__device__ inline void tile_of(int gm, int gn, int *tm, int *tn) {
+    int nb = gm * gn;
+    int b = blockIdx.x;
+    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
+    const int G = 8;
+    int per = G * gn;
+    int g = b / per;
+    int first = g * G;
+    int gs = min(gm - first, G);
+    int w = b - g * per;
+    *tm = first + w % gs;
+    *tn = w / gs;
+}
+
+// ------------------------------------------------------------------ kernel --
+
+template <int BM, int BN, int BK, int MA, int MB, int EPI, bool FAST>
+__global__ void __launch_bounds__(NTHREADS, 1)
+gemm_i8_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm, int gn) {
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && BK % 32 == 0, "tile shape");
+    constexpr int FM = BM / 64, FN = BN / 64;  // 32x32 MFMA blocks per wave
+    using LA = Layout<BM, BK>;
+    using LB = Layout<BN, BK>;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char *const ldsA = smem;                  // two stages of LA::BYTES
+    char *const ldsB = smem + 2 * LA::BYTES;  // two stages of LB::BYTES
+
+    int tm, tn;
+    tile_of(gm, gn, &tm, &tn);
+    const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
+
+    uint64_t kbeg = 0, kend = K;
+    if constexpr (EPI == EPI_PARTIAL) {
+        kbeg = (uint64_t)blockIdx.z * kslice;
+        kend = kbeg + kslice < K ? kbeg + kslice : K;
+    }
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+    [[maybe_unused]] long long wide[FM][FN][16];
+    if constexpr (EPI == EPI_WIDE) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) wide[i][j][r] = 0;
+    }
+
+    Loader<MA, BM, BK> la;
+    Loader<MB, BN, BK> lb;
+    const uint64_t nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    if (nk > 0) {
+        la.load(A, m0, kbeg, kend);
+        lb.load(B, n0, kbeg, kend);
+        la.store(ldsA);
+        lb.store(ldsB);
+    }
+    __syncthreads();
+
+    for (uint64_t kt = 0; kt < nk; ++kt) {
+        const int cur = (int)(kt & 1);
+        const bool more = kt + 1 < nk;
+        if (more) {
+            la.load(A, m0, kbeg + (kt + 1) * BK, kend);
+            lb.load(B, n0, kbeg + (kt + 1) * BK, kend);
+        }
+        const char *sa = ldsA + cur * LA::BYTES;
+        const char *sb = ldsB + cur * LB::BYTES;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            v4i af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[i] = *(const v4i *)(sa + LA::off(2 * ks + half, wm * (BM / 2) + 32 * i + l32));
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                bf[j] = *(const v4i *)(sb + LB::off(2 * ks + half, wn * (BN / 2) + 32 * j + l32));
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if constexpr (EPI == EPI_WIDE) {
+            // Fold the i32 lanes into i64 before they can hold KCHUNK terms.
+            if ((((kt + 1) * BK) % KCHUNK) == 0) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) wide[i][j][r] += acc[i][j][r];
+                        acc[i][j] = v16i{};
+                    }
+            }
+        }
+        if (more) {
+            la.store(ldsA + (cur ^ 1) * LA::BYTES);
+            lb.store(ldsB + (cur ^ 1) * LB::BYTES);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue.  MFMA output register r of lane l in a 32x32 block holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.  Each wave parks one block
+    // at a time in its own 4 KiB of LDS (free after the last barrier above)
+    // and re-reads it row-major, so the encode runs in a short rolled loop
+    // with lanes 0-31 / 32-63 on two consecutive rows.
+    int *park = (int *)smem + wave * (32 * 32 + 32);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            if constexpr (EPI == EPI_WIDE) {
+                // Two passes of 32-bit halves would lose the exact i64; the
+                // wide variant encodes from registers (its tile is one block).
+                const uint64_t col = n0 + wn * (BN / 2) + 32 * j + l32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint64_t row = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (row >= A.mn || col >= B.mn) continue;
+                    int64_t s = (int64_t)acc[i][j][r] + wide[i][j][r];
+                    char *cp = out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * out.ob;
+                    finish_any<FAST>(out, cp, s);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    park[(8 * (r >> 2) + 4 * half + (r & 3)) * 33 + l32] = acc[i][j][r];
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                __builtin_amdgcn_wave_barrier();
+                const uint64_t col = n0 + wn * (BN / 2) + 32 * j + l32;
+                const uint64_t rbase = m0 + wm * (BM / 2) + 32 * i;
+                for (int t = 0; t < 16; ++t) {
+                    const int lr = 2 * t + half;
+                    const uint64_t row = rbase + lr;
+                    const int64_t s = park[lr * 33 + l32];
+                    if (row < A.mn && col < B.mn) {
+                        if constexpr (EPI == EPI_PARTIAL) {
+                            atomicAdd((unsigned long long *)(out.work + row * B.mn + col),
+                                      (unsigned long long)s);
+                        } else {
+                            char *cp = out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * out.ob;
+                            finish_any<FAST>(out, cp, s);
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+    }
+}
+
+// The encode step over an exact partial-sum workspace (or over a zero sum
+// when k == 0: C := enc(beta * C)).
+template <bool FAST, bool ZERO>
+__global__ void __launch_bounds__(256) finish_kernel(OutArgs out, uint64_t m, uint64_t n) {
+    uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= m * n) return;
+    uint64_t row = idx / n, col = idx % n;
+    int64_t s = ZERO ? 0 : (int64_t)out.work[idx];
+    char *cp = out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * out.ob;
+    finish_any<FAST>(out, cp, s);
+}
+
+__global__ void __launch_bounds__(256) zero_i64_kernel(long long *p, uint64_t count) {
+    uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < count) p[idx] = 0;
+}
+
+// ------------------------------------------------------------------- host --
+
+template <int BM, int BN, int BK, int MA, int MB, int EPI, bool FAST>
+static hipError_t launch_tile(const Opnd &A, const Opnd &B, const OutArgs &out, uint64_t K,
+                              uint64_t kslice, int splits, hipStream_t s) {
+    constexpr int LDS = 2 * Layout<BM, BK>::BYTES + 2 * Layout<BN, BK>::BYTES;
+    auto kern = gemm_i8_kernel<BM, BN, BK, MA, MB, EPI, FAST>;
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    int gm = (int)((A.mn + BM - 1) / BM), gn = (int)((B.mn + BN - 1) / BN);
+    dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
+    hipLaunchKernelGGL(kern, grid, dim3(NTHREADS), LDS, s, A, B, out, K, kslice, gm, gn);
+    return hipGetLastError();
+}
+
+// Operand-mode pairs with a compiled kernel: (row-major A, row-major B),
+// (row-major A, column-major B), (column-major A, row-major B),
+// (column-major A, column-major B); anything else gathers.
+static int mode_pair(int ma, int mb) {
+    if (ma == LOAD_K && mb == LOAD_MN) return 0;
+    if (ma == LOAD_K && mb == LOAD_K) return 1;
+    if (ma == LOAD_MN && mb == LOAD_MN) return 2;
+    if (ma == LOAD_MN && mb == LOAD_K) return 3;
+    return 4;
+}
+
+template <int BM, int BN, int BK, int EPI, bool FAST>
+static hipError_t launch_modes(int pair, const Opnd &A, const Opnd &B, const OutArgs &out,
+                               uint64_t K, uint64_t kslice, int splits, hipStream_t s) {
+    switch (pair) {
+    case 0: return launch_tile<BM, BN, BK, LOAD_K, LOAD_MN, EPI, FAST>(A, B, out, K, kslice, splits, s);
+    case 1: return launch_tile<BM, BN, BK, LOAD_K, LOAD_K, EPI, FAST>(A, B, out, K, kslice, splits, s);
+    case 2: return launch_tile<BM, BN, BK, LOAD_MN, LOAD_MN, EPI, FAST>(A, B, out, K, kslice, splits, s);
+    case 3: return launch_tile<BM, BN, BK, LOAD_MN, LOAD_K, EPI, FAST>(A, B, out, K, kslice, splits, s);
+    default:
+        // Byte gathers need more registers than the 256-wide tile leaves.
+        if constexpr (BM <= 128)
+            return launch_tile<BM, BN, BK, LOAD_GEN, LOAD_GEN, EPI, FAST>(A, B, out, K, kslice, splits, s);
+        else
+            return hipErrorInvalidValue;
+    }
+}
+
+// The operand's load mode: vector loads need the contiguous axis to have unit
+// stride and every 16-byte chunk to start 16-byte aligned.
+static int load_mode(const Opnd &o) {
+    bool aligned = ((uintptr_t)o.base & 15) == 0;
+    if (o.s_k == 1 && aligned && (o.s_mn % 16) == 0) return LOAD_K;
+    if (o.s_mn == 1 && aligned && (o.s_k % 16) == 0) return LOAD_MN;
+    return LOAD_GEN;
+}
+
+// FAST: the int64 evaluation of alpha*sum + beta*C equals the i128 one for
+// every input of this depth (|a*b| <= 2^14).
+static bool fits_fast(int ob, uint64_t K, int64_t alpha, int64_t beta) {
+    if (ob > 8) return false;
+    long double maxsum = (long double)K * 16384.0L;
+    long double bound = fabsl((long double)alpha) * maxsum +
+                        fabsl((long double)beta) * ldexpl(1.0L, 8 * ob - 1);
+    return bound < ldexpl(1.0L, 62);
+}
+
+static uint64_t splitk_bytes(uint64_t m, uint64_t n) { return m * n * 8; }
+
+}  // namespace uor
+
+using namespace uor;
+
+extern "C" const char *uor_gfx950_status_string(int status) {
+    switch (status) {
+    case UOR_OK: return "ok";
+    case UOR_NONCONFORMANT: return "nonconformant";
+    case UOR_OUTPUT_ALIASES_ITSELF: return "output_aliases_itself";
+    case UOR_SHORT_BUFFER: return "short_buffer";
+    case UOR_INVALID_ARGUMENT: return "invalid_argument";
+    default: return status >= UOR_HIP_ERROR ? "hip_error" : "unknown";
+    }
+}
+
+extern "C" uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n) {
+    (void)k;
+    return splitk_bytes(m, n);
+}
+
+template <bool FAST>
+static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, int64_t alpha,
+                  int64_t beta, int mode, void *scratch, uint64_t scratch_bytes, hipStream_t s,
+                  uor_route *route) {
+    const uint64_t M = PA.rows, K = PA.cols, N = PB.cols;
+    Opnd A{(const int8_t *)PA.base, PA.rs, PA.cs, M};
+    Opnd B{(const int8_t *)PB.base, PB.cs, PB.rs, N};
+    OutArgs out{PC.base, PC.rs, PC.cs, ob, alpha, beta, mode, nullptr};
+    const int ma = load_mode(A), mb = load_mode(B);
+    const int pair = mode_pair(ma, mb);
+    if (route) route->operand_modes = ma | (mb << 2);
+
+    if (K == 0) {
+        // alpha * 0 + beta * C: no product, one encode per cell.
+        if (route) route->kind = UOR_ROUTE_EPILOGUE_ONLY, route->launches = 1;
+        uint64_t cells = M * N;
+        hipLaunchKernelGGL((finish_kernel<FAST, true>), dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s,
+                           out, M, N);
+        UOR_HIP(hipGetLastError());
+        return UOR_OK;
+    }
+
+    const uint64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    const uint64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    const uint64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+    const bool have_work = scratch && scratch_bytes >= splitk_bytes(M, N);
+    // Split the reduction when the output tiles alone cannot fill the 256
+    // CUs and the offer holds the exact partial sums, or when the depth
+    // exceeds one i32 lane.
+    const bool want_split = (K > (uint64_t)KCHUNK) || (t64 < 256 && K >= 8192);
+    if (want_split && have_work) {
+        const int BMN = t128 >= 64 ? 128 : 64;
+        const uint64_t tiles = BMN == 128 ? t128 : t64;
+        uint64_t splits = (1024 + tiles - 1) / tiles;
+        uint64_t min_splits = (K + KCHUNK - 1) / KCHUNK;
+        if (splits < min_splits) splits = min_splits;
+        uint64_t kslice = (K + splits - 1) / splits;
+        kslice = (kslice + 127) / 128 * 128;
+        if (kslice > (uint64_t)KCHUNK) kslice = KCHUNK;
+        splits = (K + kslice - 1) / kslice;
+        // Grid z is 16 bits; a deeper split folds in registers instead.
+        if (splits <= 65535) {
+        out.work = (long long *)scratch;
+        uint64_t cells = M * N;
+        hipLaunchKernelGGL(zero_i64_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s,
+                           out.work, cells);
+        UOR_HIP(hipGetLastError());
+        if (BMN == 128)
+            UOR_HIP((launch_modes<128, 128, 128, EPI_PARTIAL, FAST>(pair, A, B, out, K, kslice, (int)splits, s)));
+        else
+            UOR_HIP((launch_modes<64, 64, 128, EPI_PARTIAL, FAST>(pair, A, B, out, K, kslice, (int)splits, s)));
+        hipLaunchKernelGGL((finish_kernel<FAST, false>), dim3((unsigned)((cells + 255) / 256)), dim3(256), 0,
+                           s, out, M, N);
+        UOR_HIP(hipGetLastError());
+        if (route) {
+            route->kind = UOR_ROUTE_MFMA_SPLITK;
+            route->tile_m = route->tile_n = BMN;
+            route->tile_k = 128;
+            route->split_k = (int)splits;
+            route->launches = 3;
+            route->scratch_used = splitk_bytes(M, N);
+        }
+        return UOR_OK;
+        }
+    }
+    if (K > (uint64_t)KCHUNK) {
+        UOR_HIP((launch_modes<64, 64, 64, EPI_WIDE, FAST>(pair, A, B, out, K, 0, 1, s)));
+        if (route) {
+            route->kind = UOR_ROUTE_MFMA_WIDE;
+            route->tile_m = route->tile_n = 64;
+            route->tile_k = 64;
+            route->split_k = 1;
+            route->launches = 1;
+        }
+        return UOR_OK;
+    }
+    int bm;
+    if (t256 >= 256 && pair != 4) {
+        bm = 256;
+        UOR_HIP((launch_modes<256, 256, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
+    } else if (t128 >= 192) {
+        bm = 128;
+        UOR_HIP((launch_modes<128, 128, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
+    } else {
+        bm = 64;
+        UOR_HIP((launch_modes<64, 64, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
+    }
+    if (route) {
+        route->kind = UOR_ROUTE_MFMA_TILE;
+        route->tile_m = route->tile_n = bm;
+        route->tile_k = 64;
+        route->split_k = 1;
+        route->launches = 1;
+    }
+    return UOR_OK;
+}
+
+extern "C" int uor_gfx950_gemm_i8(const uor_view *a, const uor_view *b, const uor_view *c,
+                                  int out_type, int64_t alpha, int64_t beta, int encode,
+                                  void *scratch, uint64_t scratch_bytes, void *stream,
+                                  uor_route *route) {
+    route_set(route, UOR_ROUTE_NONE);
+    if (!valid_out_type(out_type) || !valid_encode(encode)) return UOR_INVALID_ARGUMENT;
+    Placed A, B, C;
+    int st = make_triple(a, 1, b, 1, c, out_type, &A, &B, &C);
+    if (st) return st;
+    if (C.rows == 0 || C.cols == 0) return UOR_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (fits_fast(out_type, A.cols, alpha, beta))
+        return run_i8<true>(A, B, C, out_type, alpha, beta, encode, scratch, scratch_bytes, s, route);
+    return run_i8<false>(A, B, C, out_type, alpha, beta, encode, scratch, scratch_bytes, s, route);
+}
+
+extern "C" int uor_gfx950_slice_gemm_ex_i8(uint64_t m, uint64_t k, uint64_t n, int64_t alpha,
+                                           const int8_t *a, uint64_t a_len, uint64_t lda,
+                                           const int8_t *b, uint64_t b_len, uint64_t ldb,
+                                           int64_t beta, void *c, uint64_t c_len, uint64_t ldc,
+                                           int out_type, void *scratch, uint64_t scratch_bytes,
+                                           void *stream) {
+    // slice.rs:87 ld(): row-major strides {rs: ld, cs: 1}.
+    uor_view av{(void *)a, a_len, m, k, (int64_t)lda, 1};
+    uor_view bv{(void *)b, b_len, k, n, (int64_t)ldb, 1};
+    uor_view cv{c, c_len, m, n, (int64_t)ldc, 1};
+    return uor_gfx950_gemm_i8(&av, &bv, &cv, out_type, alpha, beta, UOR_ENCODE_NEAREST, scratch,
+                              scratch_bytes, stream, nullptr);
+}
+
+extern "C" int uor_gfx950_slice_gemm_i8(uint64_t m, uint64_t k, uint64_t n, const int8_t *a,
+                                        uint64_t a_len, const int8_t *b, uint64_t b_len, void *c,
+                                        uint64_t c_len, int out_type, void *scratch,
+                                        uint64_t scratch_bytes, void *stream) {
+    return uor_gfx950_slice_gemm_ex_i8(m, k, n, 1, a, a_len, k, b, b_len, n, 0, c, c_len, n,
+                                       out_type, scratch, scratch_bytes, stream);
+}

@@ -1,0 +1,222 @@
+"""ctypes binding of libuor_gfx950.so (the C ABI in include/uor_gfx950.h).
+
+Buffers are device tensors from PyTorch (used only for device memory and
+streams); every computation runs in the library's HIP kernels.  Loading fails
+loudly when the library has not been built: there is no other route.
+
+Import torch before this module so the library binds to the HIP runtime torch
+already loaded (both carry the SONAME libamdhip64.so.7).
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libuor_gfx950.so"
+
+OUT = {"i8": 1, "i16": 2, "i32": 4, "i64": 8, "i128": 16}
+ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
+STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
+          4: "invalid_argument"}
+ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
+          10: "lut4_dot4", 20: "float_crt", 21: "float_direct", 30: "trop_valu"}
+
+# Every symbol include/uor_gfx950.h declares.
+SYMBOLS = [
+    "uor_gfx950_status_string",
+    "uor_gfx950_gemm_i8",
+    "uor_gfx950_slice_gemm_ex_i8",
+    "uor_gfx950_slice_gemm_i8",
+    "uor_gfx950_suggested_scratch_i8",
+    "uor_gfx950_gemm_lut4",
+    "uor_gfx950_gemm_float",
+    "uor_gfx950_slice_gemm_float_ex",
+    "uor_gfx950_sgemm",
+    "uor_gfx950_dgemm",
+    "uor_gfx950_suggested_scratch_float",
+    "uor_gfx950_gemm_trop_i8",
+]
+
+
+class View(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("len", ctypes.c_uint64), ("rows", ctypes.c_uint64),
+                ("cols", ctypes.c_uint64), ("rs", ctypes.c_int64), ("cs", ctypes.c_int64)]
+
+
+class Route(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("tile_m", ctypes.c_int32), ("tile_n", ctypes.c_int32),
+                ("tile_k", ctypes.c_int32), ("split_k", ctypes.c_int32),
+                ("launches", ctypes.c_int32), ("operand_modes", ctypes.c_int32),
+                ("moduli", ctypes.c_int32), ("scratch_used", ctypes.c_uint64)]
+
+    def as_dict(self):
+        d = {f: getattr(self, f) for f, _ in self._fields_}
+        d["kind"] = ROUTES.get(self.kind, self.kind)
+        return d
+
+
+_u64, _i64, _i32, _vp = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+_PV = ctypes.POINTER(View)
+_PR = ctypes.POINTER(Route)
+_lib = None
+
+
+class UorError(RuntimeError):
+    def __init__(self, status):
+        self.status = status
+        super().__init__(f"uor_gfx950 status {status} ({STATUS.get(status, 'hip_error')})")
+
+
+def lib():
+    """The loaded C ABI.  Raises if libuor_gfx950.so is missing."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} is not built; run `python uor-matmul_amd/build.py` "
+                "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.uor_gfx950_status_string.argtypes = [_i32]
+        L.uor_gfx950_status_string.restype = ctypes.c_char_p
+        L.uor_gfx950_gemm_i8.argtypes = [_PV, _PV, _PV, _i32, _i64, _i64, _i32, _vp, _u64, _vp, _PR]
+        L.uor_gfx950_gemm_i8.restype = _i32
+        L.uor_gfx950_slice_gemm_ex_i8.argtypes = [_u64, _u64, _u64, _i64, _vp, _u64, _u64, _vp,
+                                                  _u64, _u64, _i64, _vp, _u64, _u64, _i32, _vp,
+                                                  _u64, _vp]
+        L.uor_gfx950_slice_gemm_ex_i8.restype = _i32
+        L.uor_gfx950_slice_gemm_i8.argtypes = [_u64, _u64, _u64, _vp, _u64, _vp, _u64, _vp, _u64,
+                                               _i32, _vp, _u64, _vp]
+        L.uor_gfx950_slice_gemm_i8.restype = _i32
+        L.uor_gfx950_suggested_scratch_i8.argtypes = [_u64, _u64, _u64]
+        L.uor_gfx950_suggested_scratch_i8.restype = _u64
+        if hasattr(L, "uor_gfx950_gemm_lut4"):
+            L.uor_gfx950_gemm_lut4.argtypes = [_PV, _vp, _u64, _u64, _vp, _u64, _u64, _PV, _i32,
+                                               _i64, _i64, _i32, _vp, _u64, _vp, _PR]
+            L.uor_gfx950_gemm_lut4.restype = _i32
+        if hasattr(L, "uor_gfx950_gemm_float"):
+            L.uor_gfx950_gemm_float.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32, _vp, _u64,
+                                                _vp, _PR]
+            L.uor_gfx950_gemm_float.restype = _i32
+            L.uor_gfx950_slice_gemm_float_ex.argtypes = [_i32, _u64, _u64, _u64, _i64, _vp, _u64,
+                                                         _u64, _vp, _u64, _u64, _i64, _vp, _u64,
+                                                         _u64, _vp, _u64, _vp]
+            L.uor_gfx950_slice_gemm_float_ex.restype = _i32
+            for name in ("uor_gfx950_sgemm", "uor_gfx950_dgemm"):
+                f = getattr(L, name)
+                f.argtypes = [_u64, _u64, _u64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                              _vp, _i64, _i64, _vp, _u64, _vp]
+                f.restype = _i32
+            L.uor_gfx950_suggested_scratch_float.argtypes = [_i32, _u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_float.restype = _u64
+        if hasattr(L, "uor_gfx950_gemm_trop_i8"):
+            L.uor_gfx950_gemm_trop_i8.argtypes = [_PV, _PV, _PV, _i32, _i64, _i32, _i64, _i32,
+                                                  _i32, _vp, _u64, _vp, _PR]
+            L.uor_gfx950_gemm_trop_i8.restype = _i32
+        _lib = L
+    return _lib
+
+
+def _ptr(t):
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(stream):
+    if stream is not None:
+        return stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def view(buf, rows, cols, rs, cs, rec=1):
+    """A uor_view over the flat device tensor `buf` (its length in elements
+    is buf.numel() // rec, for record types spelled as bytes)."""
+    return View(_ptr(buf), buf.numel() // rec, rows, cols, rs, cs)
+
+
+def gemm_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+            out="i32", alpha=1, beta=0, encode="nearest", scratch=None, stream=None):
+    """The view API at E = i8.  Returns (status, route dict).  `c` is a flat
+    device tensor of the output type (int8/16/32/64, or int64 pairs for i128)."""
+    ob = OUT[out]
+    rec = 2 if ob == 16 else 1
+    av = view(a, *a_shape, *a_strides)
+    bv = view(b, *b_shape, *b_strides)
+    cv = view(c, *c_shape, *c_strides, rec=rec)
+    r = Route()
+    st = lib().uor_gfx950_gemm_i8(ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob,
+                                  int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
+                                  0 if scratch is None else scratch.numel() * scratch.element_size(),
+                                  _stream(stream), ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def slice_gemm_ex_i8(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, out="i32", scratch=None,
+                     stream=None):
+    ob = OUT[out]
+    return lib().uor_gfx950_slice_gemm_ex_i8(
+        m, k, n, int(alpha), _ptr(a), a.numel(), lda, _ptr(b), b.numel(), ldb, int(beta),
+        _ptr(c), c.numel() // (2 if ob == 16 else 1), ldc, ob, _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+
+
+def slice_gemm_i8(m, k, n, a, b, c, out="i32", scratch=None, stream=None):
+    ob = OUT[out]
+    return lib().uor_gfx950_slice_gemm_i8(
+        m, k, n, _ptr(a), a.numel(), _ptr(b), b.numel(), _ptr(c),
+        c.numel() // (2 if ob == 16 else 1), ob, _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+
+
+def suggested_scratch_i8(m, k, n):
+    return lib().uor_gfx950_suggested_scratch_i8(m, k, n)
+
+
+def gemm_lut4(a, m, k, a_strides, codes, n, books, group, c, c_strides, out="i32", alpha=1,
+              beta=0, encode="nearest", scratch=None, stream=None):
+    ob = OUT[out]
+    av = view(a, m, k, *a_strides)
+    cv = view(c, m, n, *c_strides, rec=2 if ob == 16 else 1)
+    r = Route()
+    st = lib().uor_gfx950_gemm_lut4(
+        ctypes.byref(av), _ptr(codes), codes.numel(), n, _ptr(books), books.numel(), group,
+        ctypes.byref(cv), ob, int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def gemm_float(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides, alpha=1,
+               beta=0, encode="nearest", scratch=None, stream=None):
+    import torch
+    is64 = int(a.dtype == torch.float64)
+    av = view(a, *a_shape, *a_strides)
+    bv = view(b, *b_shape, *b_strides)
+    cv = view(c, *c_shape, *c_strides)
+    r = Route()
+    st = lib().uor_gfx950_gemm_float(
+        is64, ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), int(alpha), int(beta),
+        ENCODE[encode], _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def suggested_scratch_float(is64, m, k, n):
+    return lib().uor_gfx950_suggested_scratch_float(int(is64), m, k, n)
+
+
+def gemm_trop_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides, out=4,
+                 alpha=(0, True), beta=(0, False), encode="nearest", scratch=None, stream=None):
+    """a, b: uint8 device tensors of 2-byte Trop<i8> records; c: uint8 tensor of
+    2*out-byte Trop<out> records."""
+    av = view(a, *a_shape, *a_strides, rec=2)
+    bv = view(b, *b_shape, *b_strides, rec=2)
+    cv = view(c, *c_shape, *c_strides, rec=2 * out)
+    r = Route()
+    st = lib().uor_gfx950_gemm_trop_i8(
+        ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), out, int(alpha[0]),
+        int(bool(alpha[1])), int(beta[0]), int(bool(beta[1])), ENCODE[encode], _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ctypes.byref(r))
+    return st, r.as_dict()
