@@ -149,3 +149,32 @@ def trop_i8(values, finite):
 
 def trop_bytes(rec):
     return np.ascontiguousarray(rec).view(np.uint8).reshape(-1)
+
+
+# ------------------------------------------------------------ CPU baseline
+FAST = HERE / "libfastroute.so"
+_fast = None
+
+
+def fast():
+    """The CPU baseline (oracle/fastroute.cpp): the reference's fast routes
+    restated in C++, timed beside the GPU by bench.py."""
+    global _fast
+    if _fast is None:
+        if not FAST.exists():
+            build()
+        F = ctypes.CDLL(str(FAST))
+        F.fr_has_vnni.restype = _i32
+        F.fr_hw_threads.restype = _i32
+        F.fr_gemm_i8_i32.argtypes = [_i32, _i32, _i32, _i64, _vp, _i64, _vp, _i64, _i64, _vp,
+                                     _i64, _i32, _i32, _i32, _i32]
+        F.fr_gemm_i8_i32.restype = _i32
+        _fast = F
+    return _fast
+
+
+def fast_gemm_i8_i32(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, row0=0, rows=None,
+                     threads=1, force_avx2=False):
+    rows = m if rows is None else rows
+    return fast().fr_gemm_i8_i32(m, k, n, int(alpha), _ptr(a), lda, _ptr(b), ldb, int(beta),
+                                 _ptr(c), ldc, row0, rows, threads, int(force_avx2))

@@ -149,13 +149,19 @@ __device__ static inline i128 encode_int(i128 v, int bytes, int mode) {
 __device__ static inline i128 sat_mul(i128 x, int64_t f) {
     const i128 MX = (i128)(((u128)1 << 127) - 1), MN = (i128)((u128)1 << 127);
     if (x == 0 || f == 0) return 0;
-    u128 ax = x < 0 ? (u128)0 - (u128)x : (u128)x;
-    u128 af = f < 0 ? (u128)0 - (u128)(i128)f : (u128)(i128)f;
-    bool neg = (x < 0) != (f < 0);
-    // |x| * |f| overflows i128 iff it exceeds the bound for its sign.
-    u128 limit = neg ? ((u128)1 << 127) : (((u128)1 << 127) - 1);
-    if (ax > limit / af) return neg ? MN : MX;
-    u128 p = ax * af;
+    const bool neg = (x < 0) != (f < 0);
+    const u128 ax = x < 0 ? (u128)0 - (u128)x : (u128)x;
+    const uint64_t af = f < 0 ? (uint64_t)0 - (uint64_t)f : (uint64_t)f;
+    // |x| * |f| as a 192-bit product (top : p), without a 128-bit division.
+    const uint64_t a0 = (uint64_t)ax, a1 = (uint64_t)(ax >> 64);
+    const uint64_t lo = a0 * af, c0 = __umul64hi(a0, af);
+    const uint64_t m1 = a1 * af, h1 = __umul64hi(a1, af);
+    const uint64_t mid = m1 + c0;
+    const uint64_t top = h1 + (mid < m1 ? 1 : 0);
+    const u128 p = ((u128)mid << 64) | lo;
+    // It overflows i128 iff it exceeds the bound for its sign.
+    const u128 limit = neg ? ((u128)1 << 127) : (((u128)1 << 127) - 1);
+    if (top != 0 || p > limit) return neg ? MN : MX;
     return neg ? (i128)((u128)0 - p) : (i128)p;
 }
 

@@ -22,6 +22,11 @@
 // the chunk-stride pad keep the 64 lanes on distinct banks for both the
 // fragment reads and the transposing dword writes.
 
+#include <stdlib.h>
+#include <string.h>
+
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace uor {
@@ -219,6 +224,66 @@ __device__ inline void finish_any(const OutArgs &o, char *cp, int64_t sum) {
     }
 }
 
+// Encode one 32x32 accumulator block parked row-major in LDS (row stride 33
+// ints) into C.  Lanes 0-31 / 32-63 take columns l32 of rows 2t / 2t+1.
+// The C values of a batch are all loaded before any is stored, so their
+// loads are in flight together instead of one latency per cell.
+template <int OB, bool FAST>
+__device__ inline void encode_block(const OutArgs &o, const int *park, uint64_t rbase,
+                                    uint64_t col, uint64_t M, uint64_t N) {
+    const int lane = threadIdx.x & 63, half = lane >> 5, l32 = lane & 31;
+    if (col >= N) return;
+    char *const cbase = o.base + (int64_t)col * o.cs * OB;
+    const int64_t rstride = o.rs * OB;
+    if constexpr (FAST && OB <= 8) {
+        int64_t prior[16];
+        if (o.beta != 0) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const uint64_t row = rbase + 2 * t + half;
+                prior[t] = row < M ? (int64_t)load_out<OB>(cbase + (int64_t)row * rstride) : 0;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int lr = 2 * t + half;
+            const uint64_t row = rbase + lr;
+            if (row >= M) continue;
+            int64_t x = (int64_t)park[lr * 33 + l32] * o.alpha;
+            if (o.beta != 0) x += prior[t] * o.beta;
+            store_out<OB>(cbase + (int64_t)row * rstride, encode_int((i128)x, OB, o.mode));
+        }
+    } else {
+        // The full i128 evaluation (huge alpha/beta, or an i128 output): kept
+        // rolled and unbatched, so it costs few registers in the kernel.
+#pragma unroll 1
+        for (int t = 0; t < 16; ++t) {
+            const int lr = 2 * t + half;
+            const uint64_t row = rbase + lr;
+            if (row >= M) continue;
+            char *cp = cbase + (int64_t)row * rstride;
+            i128 x = sat_mul((i128)park[lr * 33 + l32], o.alpha);
+            if (o.beta != 0) x = (i128)((u128)x + (u128)sat_mul(load_out<OB>(cp), o.beta));
+            store_out<OB>(cp, encode_int(x, OB, o.mode));
+        }
+    }
+}
+
+// Add one parked 32x32 block into the exact partial-sum workspace.
+__device__ inline void partial_block(const OutArgs &o, const int *park, uint64_t rbase,
+                                     uint64_t col, uint64_t M, uint64_t N) {
+    const int lane = threadIdx.x & 63, half = lane >> 5, l32 = lane & 31;
+    if (col >= N) return;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int lr = 2 * t + half;
+        const uint64_t row = rbase + lr;
+        if (row < M)
+            atomicAdd((unsigned long long *)(o.work + row * N + col),
+                      (unsigned long long)(int64_t)park[lr * 33 + l32]);
+    }
+}
+
 // Tile index -> (tile row, tile column).  Workgroups are dealt round-robin to
 // the 8 XCDs, so consecutive ids are remapped onto one XCD first, then walked
 // in groups of 8 tile rows so that the tiles one XCD holds at a time share
@@ -364,22 +429,312 @@ gemm_i8_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm,
                 __builtin_amdgcn_wave_barrier();
                 const uint64_t col = n0 + wn * (BN / 2) + 32 * j + l32;
                 const uint64_t rbase = m0 + wm * (BM / 2) + 32 * i;
-                for (int t = 0; t < 16; ++t) {
-                    const int lr = 2 * t + half;
-                    const uint64_t row = rbase + lr;
-                    const int64_t s = park[lr * 33 + l32];
-                    if (row < A.mn && col < B.mn) {
-                        if constexpr (EPI == EPI_PARTIAL) {
-                            atomicAdd((unsigned long long *)(out.work + row * B.mn + col),
-                                      (unsigned long long)s);
-                        } else {
-                            char *cp = out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * out.ob;
-                            finish_any<FAST>(out, cp, s);
-                        }
+                if constexpr (EPI == EPI_PARTIAL) {
+                    partial_block(out, park, rbase, col, A.mn, B.mn);
+                } else if (col < B.mn) {
+                    // Rolled, one cell at a time: the generic-layout kernels
+                    // keep their registers for the gathering loaders.
+                    for (int t = 0; t < 16; ++t) {
+                        const int lr = 2 * t + half;
+                        const uint64_t row = rbase + lr;
+                        if (row >= A.mn) continue;
+                        char *cp = out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * out.ob;
+                        finish_any<FAST>(out, cp, park[lr * 33 + l32]);
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
             }
+        }
+    }
+}
+
+// ------------------------------------------------- direct-to-LDS pipeline --
+//
+// The row-major x row-major case (A's reduction axis contiguous, B's n axis
+// contiguous) with k a multiple of 64 and n of 16 streams both operands
+// straight from global memory into LDS (global_load_lds_dwordx4: lane L of an
+// instruction lands at base + 16*L), NSTAGE stages deep, so each wave keeps
+// three k-steps of loads in flight while its MFMAs run.  B stays row-major
+// ([k][n]) in LDS and reaches the MFMA through ds_read_b64_tr_b8, which
+// transposes 8x8 bytes across each 16-lane group: output lane t, byte b is
+// byte t%8 of the row addressed by lane 2b + t/8.
+//
+// LDS swizzles (16-byte granularity) keep every read pass on distinct banks:
+//   A stage: row r, k-chunk c at r*64 + 16*(c ^ ((r >> 2) & 3))
+//   B stage: k-row k, n-chunk x at k*BN + 16*(x ^ (2*(k & 7) & (BN/16 - 1)))
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+typedef __attribute__((address_space(3))) void lds_void;
+
+#ifndef UOR_DL_ASM
+#define UOR_DL_ASM 1
+#endif
+
+constexpr int DL_BK = 64;
+constexpr int DL_NSTAGE = 4;
+
+template <int BM, int BN>
+struct DlLayout {
+    static constexpr int A_BYTES = BM * DL_BK;
+    static constexpr int B_BYTES = BN * DL_BK;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int BYTES = DL_NSTAGE * STAGE;
+    __device__ static inline int a_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+    __device__ static inline int b_swz(int k) { return (2 * (k & 7)) & (BN / 16 - 1); }
+    __device__ static inline int b_off(int k, int x) { return k * BN + 16 * (x ^ b_swz(k)); }
+};
+
+template <int N>
+__device__ inline void wait_vm() {
+    // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt split in [3:0] and [15:14]),
+    // leaving expcnt and lgkmcnt unconstrained.
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// A workgroup barrier without the release fence __syncthreads() carries: the
+// fence would wait for every LDS-DMA load in flight (all stages), while each
+// thread has already waited (vmcnt) for the one stage the next step reads.
+// The empty asm statements keep the compiler from moving LDS accesses across.
+__device__ inline void stage_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// One 16-byte-per-lane global -> LDS load: lane L's 16 bytes land at
+// lds + 16*L.  Issued through inline assembly so the compiler's wait
+// insertion, which cannot tell the four stages apart across the loop's back
+// edge, does not drain every stage before a read; the explicit vmcnt waits in
+// the k loop order each stage instead.
+// M0 is reserved by the compiler, which warns on the clobber; the kernels that
+// call this make no other use of M0 (checked in their ISA).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void lds_dma16(const int8_t *g, char *lds) {
+#if UOR_DL_ASM
+    const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(l)), "v"(g)
+                 : "memory", "m0");
+#else
+    __builtin_amdgcn_global_load_lds((const void *)g, (lds_void *)lds, 16, 0, 0);
+#endif
+}
+#pragma clang diagnostic pop
+
+template <int BM, int BN, int NT>
+__device__ inline void dl_issue(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t k0,
+                                char *stage) {
+    using L = DlLayout<BM, BN>;
+    constexpr int PA = BM * 4 / NT, PB = BN * 4 / NT;  // 16-byte chunks per thread
+    static_assert(PA >= 1 && PB >= 1, "tile too small for the workgroup");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // A: BM*4 chunks, slot s = row*4 + physical chunk.
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+        const int base = (wave * PA + i) * 64;
+        const int slot = base + lane;
+        const int row = slot >> 2, pc = slot & 3;
+        const int c = pc ^ ((row >> 2) & 3);
+        uint64_t gr = m0 + row;
+        if (gr >= A.mn) gr = A.mn - 1;  // rows past m are computed and discarded
+        lds_dma16(A.base + (int64_t)gr * A.s_mn + (int64_t)(k0 + 16 * c), stage + base * 16);
+    }
+    // B: BN/16 chunks per k-row, slot s = k*(BN/16) + physical chunk.
+    char *bst = stage + L::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+        const int base = (wave * PB + i) * 64;
+        const int slot = base + lane;
+        const int k = slot / (BN / 16), px = slot % (BN / 16);
+        const int x = px ^ L::b_swz(k);
+        uint64_t gn = n0 + 16 * x;
+        if (gn >= B.mn) gn = 0;  // columns past n are computed and discarded
+        lds_dma16(B.base + (int64_t)(k0 + k) * B.s_k + (int64_t)gn, bst + base * 16);
+    }
+}
+
+// One k-step of 64 from LDS stage `sa` (A) / `sb` (B): each wave's FM x FN
+// 32x32 blocks, two 32-deep MFMAs each.
+template <int BM, int BN, int WM, int WN>
+__device__ inline void dl_compute(const char *sa, const char *sb,
+                                  v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    using L = DlLayout<BM, BN>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int half = lane >> 5, l32 = lane & 31;
+    const int grp = lane >> 4, t16 = lane & 15;
+    v4i af[2][FM];
+    v4i bf[2][FN];
+#pragma unroll
+    for (int ks = 0; ks < DL_BK / 32; ++ks) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            af[ks][i] = *(const v4i *)(sa + L::a_off(wm * (BM / WM) + 32 * i + l32, 2 * ks + half));
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int nb = wn * (BN / WN) + 32 * j + 16 * (grp & 1) + 8 * (t16 & 1);
+            const int k = 32 * ks + 16 * (grp >> 1) + (t16 >> 1);
+            v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_v2i *)(sb + L::b_off(k, nb >> 4) + (nb & 8)));
+            v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_v2i *)(sb + L::b_off(k + 8, nb >> 4) + (nb & 8)));
+            bf[ks][j] = v4i{lo[0], lo[1], hi[0], hi[1]};
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < DL_BK / 32; ++ks)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+}
+
+// WM x WN waves of 64 lanes (4 waves: one per SIMD, 128x128 each at BM=BN=256;
+// 8 waves: two per SIMD, so one wave's LDS reads overlap the other's MFMAs).
+template <int BM, int BN, int WM, int WN, int EPI, bool FAST, int OB>
+__global__ void __launch_bounds__(64 * WM * WN, 1)
+gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm, int gn) {
+    constexpr int NT = 64 * WM * WN;
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    using L = DlLayout<BM, BN>;
+    constexpr int LOADS = (BM + BN) * 4 / NT;  // global_load_lds per thread per stage
+    static_assert(DL_NSTAGE == 4, "the k loop below is unrolled by four stages");
+    static_assert(WM * WN * (32 * 33) * 4 <= 2 * L::STAGE, "epilogue parking fits two stages");
+    // One LDS object per stage, so that every read names the stage it reads.
+    __shared__ __attribute__((aligned(16))) char st0[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char st1[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char st2[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char st3[L::STAGE];
+
+    int tm, tn;
+    tile_of(gm, gn, &tm, &tn);
+    const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
+    uint64_t kbeg = 0, kend = K;
+    if constexpr (EPI == EPI_PARTIAL) {
+        kbeg = (uint64_t)blockIdx.z * kslice;
+        kend = kbeg + kslice < K ? kbeg + kslice : K;
+    }
+    const int nk = (int)((kend - kbeg) / DL_BK);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+    if (0 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg, st0);
+    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + DL_BK, st1);
+    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + 2 * DL_BK, st2);
+
+    // Step kt reads stage kt % 4 and refills stage (kt + 3) % 4, last read at
+    // step kt - 1, which every wave has finished once it passes the barrier.
+#define UOR_DL_STEP(CUR, NXT)                                                                  \
+    {                                                                                          \
+        const int ahead = min(DL_NSTAGE - 2, nk - 1 - kt);                                     \
+        if (ahead >= 2) wait_vm<2 * LOADS>();                                                  \
+        else if (ahead == 1) wait_vm<LOADS>();                                                 \
+        else wait_vm<0>();                                                                     \
+        stage_barrier();                                                                       \
+        if (kt + DL_NSTAGE - 1 < nk)                                                           \
+            dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + (uint64_t)(kt + DL_NSTAGE - 1) * DL_BK, NXT); \
+        dl_compute<BM, BN, WM, WN>(CUR, CUR + L::A_BYTES, acc);                                \
+        if (++kt >= nk) break;                                                                 \
+    }
+    for (int kt = 0; kt < nk;) {
+        UOR_DL_STEP(st0, st3)
+        UOR_DL_STEP(st1, st0)
+        UOR_DL_STEP(st2, st1)
+        UOR_DL_STEP(st3, st2)
+    }
+#undef UOR_DL_STEP
+    wait_vm<0>();
+    __syncthreads();
+
+    if constexpr (EPI == EPI_FUSED && FAST && OB <= 4 && WM * WN == 8 && FM * FN == 8) {
+        // All four stages are free now: each wave parks four 32x32 blocks
+        // (16 KiB, row stride 32 ints with the column XOR-swizzled by row bit
+        // 2 against bank conflicts) and loads their 64 C values per lane in
+        // one batch, so a tile costs two memory round trips per wave.
+        char *region = wave < 2 ? st0 : wave < 4 ? st1 : wave < 6 ? st2 : st3;
+        int *park4 = (int *)(region + (wave & 1) * 16384);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            // Blocks q = 0..3 of this batch are (i, j) = (2g + q/2, q%2).
+            int32_t prior[4][16];
+            if (out.beta != 0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = 2 * g + q / 2, j = q % 2;
+                    const uint64_t col = n0 + wn * (BN / WN) + 32 * j + l32;
+                    const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) {
+                        const uint64_t row = rbase + 2 * t + half;
+                        prior[q][t] = (row < A.mn && col < B.mn)
+                                          ? (int32_t)load_out<OB>(out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * OB)
+                                          : 0;
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = 2 * g + q / 2, j = q % 2;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+                    park4[q * 1024 + row * 32 + (l32 ^ (((row >> 2) & 1) << 4))] = acc[i][j][r];
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = 2 * g + q / 2, j = q % 2;
+                const uint64_t col = n0 + wn * (BN / WN) + 32 * j + l32;
+                const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
+                if (col >= B.mn) continue;
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const int lr = 2 * t + half;
+                    const uint64_t row = rbase + lr;
+                    if (row >= A.mn) continue;
+                    int64_t x = (int64_t)park4[q * 1024 + lr * 32 + (l32 ^ (((lr >> 2) & 1) << 4))] * out.alpha;
+                    if (out.beta != 0) x += (int64_t)prior[q][t] * out.beta;
+                    store_out<OB>(out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * OB,
+                                  encode_int((i128)x, OB, out.mode));
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
+
+    // Waves 0..3 park in stage 0, waves 4..7 in stage 1.
+    int *park = (int *)(wave < 4 ? st0 : st1) + (wave & 3) * (32 * 33);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                park[(8 * (r >> 2) + 4 * half + (r & 3)) * 33 + l32] = acc[i][j][r];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            const uint64_t col = n0 + wn * (BN / WN) + 32 * j + l32;
+            const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
+            if constexpr (EPI == EPI_PARTIAL) partial_block(out, park, rbase, col, A.mn, B.mn);
+            else encode_block<OB, FAST>(out, park, rbase, col, A.mn, B.mn);
+            __builtin_amdgcn_wave_barrier();
         }
     }
 }
@@ -419,6 +774,43 @@ static hipError_t launch_tile(const Opnd &A, const Opnd &B, const OutArgs &out, 
     dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
     hipLaunchKernelGGL(kern, grid, dim3(NTHREADS), LDS, s, A, B, out, K, kslice, gm, gn);
     return hipGetLastError();
+}
+
+
+template <int BM, int BN, int WM, int WN, int EPI, bool FAST>
+static hipError_t launch_dl(const Opnd &A, const Opnd &B, const OutArgs &out, uint64_t K,
+                            uint64_t kslice, int splits, hipStream_t s) {
+    auto kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 4>;
+    if constexpr (EPI != EPI_PARTIAL) {
+        switch (out.ob) {
+        case 1: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 1>; break;
+        case 2: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 2>; break;
+        case 8: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 8>; break;
+        case 16: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, false, 16>; break;
+        default: break;
+        }
+    }
+    int gm = (int)((A.mn + BM - 1) / BM), gn = (int)((B.mn + BN - 1) / BN);
+    dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), 0, s, A, B, out, K, kslice, gm, gn);
+    return hipGetLastError();
+}
+
+// The direct-to-LDS pipeline applies when both operands stream in 16-byte
+// chunks along their contiguous axes and every chunk is whole: k a multiple
+// of its 64-byte step (of the split slice too) and n of 16.
+// Which 256x256 pipeline runs (UOR_GFX950_DL_VARIANT = w8 | w4 at load time;
+// w8 by default): 8 waves (two per SIMD) or 4 waves (one per SIMD).
+static int dl_variant() {
+    static int v = [] {
+        const char *e = getenv("UOR_GFX950_DL_VARIANT");
+        return (e && !strcmp(e, "w4")) ? 4 : 8;
+    }();
+    return v;
+}
+
+static bool dl_ok(int pair, uint64_t K, uint64_t N) {
+    return pair == 0 && K % DL_BK == 0 && N % 16 == 0;
 }
 
 // Operand-mode pairs with a compiled kernel: (row-major A, row-major B),
@@ -537,7 +929,9 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         hipLaunchKernelGGL(zero_i64_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s,
                            out.work, cells);
         UOR_HIP(hipGetLastError());
-        if (BMN == 128)
+        if (BMN == 128 && dl_ok(pair, K, N) && kslice % DL_BK == 0)
+            UOR_HIP((launch_dl<128, 128, 2, 2, EPI_PARTIAL, FAST>(A, B, out, K, kslice, (int)splits, s)));
+        else if (BMN == 128)
             UOR_HIP((launch_modes<128, 128, 128, EPI_PARTIAL, FAST>(pair, A, B, out, K, kslice, (int)splits, s)));
         else
             UOR_HIP((launch_modes<64, 64, 128, EPI_PARTIAL, FAST>(pair, A, B, out, K, kslice, (int)splits, s)));
@@ -567,9 +961,18 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         return UOR_OK;
     }
     int bm;
-    if (t256 >= 256 && pair != 4) {
+    if (t256 >= 256 && dl_ok(pair, K, N)) {
         bm = 256;
-        UOR_HIP((launch_modes<256, 256, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
+        if (dl_variant() == 4)
+            UOR_HIP((launch_dl<256, 256, 2, 2, EPI_FUSED, FAST>(A, B, out, K, 0, 1, s)));
+        else
+            UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST>(A, B, out, K, 0, 1, s)));
+        if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline
+    } else if (FAST && t256 >= 256 && pair != 4) {
+        // (The i128 epilogue does not fit beside a 256-wide generic tile's
+        // registers; those requests take the 128-wide tile below.)
+        bm = 256;
+        if constexpr (FAST) UOR_HIP((launch_modes<256, 256, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
     } else if (t128 >= 192) {
         bm = 128;
         UOR_HIP((launch_modes<128, 128, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));

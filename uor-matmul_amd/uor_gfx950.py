@@ -10,10 +10,12 @@ already loaded (both carry the SONAME libamdhip64.so.7).
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 
 HERE = pathlib.Path(__file__).resolve().parent
-LIB_PATH = HERE / "libuor_gfx950.so"
+# UOR_GFX950_LIB points the binding at another build of the same ABI.
+LIB_PATH = pathlib.Path(os.environ.get("UOR_GFX950_LIB", HERE / "libuor_gfx950.so"))
 
 OUT = {"i8": 1, "i16": 2, "i32": 4, "i64": 8, "i128": 16}
 ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
