@@ -137,6 +137,52 @@ def bench_i8(args, torch, uor, gen):
     return result, (a, b, c0)
 
 
+def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
+    """the 4-bit LUT decode GEMM, m in {1, 8, 32}, k = 8192,
+    n = 28672, one codebook per 128 coded rows.  Three distinct code buffers
+    (3 x 117 MB, beyond the 256 MB Infinity Cache) rotate across steps so the
+    codes stream from HBM.  GB/s counts algorithmic bytes:
+    n*k/2 + m*k + 4*m*n + books."""
+    k, n, group = 8192, 28672, 128
+    dev = torch.device("cuda:0")
+    codes = [torch.from_numpy(gen.i8_full(n * k // 2, 7 + 100 * r).view("uint8")).to(dev)
+             for r in range(3)]
+    books = torch.from_numpy(gen.i8_full((n // group) * 16, 8)).to(dev)
+    out = []
+    stream = torch.cuda.current_stream()
+    for m in ms_list:
+        a = torch.from_numpy(gen.i8_full(m * k, 6)).to(dev)
+        c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+        route = {}
+
+        def step(i):
+            st, r = uor.gemm_lut4(a, m, k, (k, 1), codes[i % 3], n, books, group, c, (n, 1),
+                                  stream=stream.cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"lut4 status {st}")
+            route.update(r)
+
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        steps = max(args.steps, 30)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for i in range(steps):
+            step(i)
+        s1.record(stream)
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / steps
+        nbytes = n * k // 2 + m * k + 4 * m * n + (n // group) * 16
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"m": m, "k": k, "n": n, "group": group, "ms_per_call": round(ms, 5),
+                    "GB_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                    "TOPS": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
+                    "algorithmic_bytes": nbytes,
+                    "kernel": "lut4_dot4_kernel" if m <= 4 else "lut4_mfma_kernel"})
+    return out
+
+
 def cpu_baseline_i8(host, oracle):
     """The reference's packed route restated (oracle/fastroute.cpp) on a row
     slab of the same 8192^3 problem, all usable host cores."""
@@ -179,6 +225,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-lut", action="store_true", help="skip the secondary LUT decode figure")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device-to-device copy and exit (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -201,6 +248,17 @@ def main():
     import gen
     uor.lib()
     result, host = bench_i8(args, torch, uor, gen)
+    if not args.no_lut:
+        log("[bench] lut4 decode")
+        lut = bench_lut4(args, torch, uor, gen)
+        result["secondary"] = {
+            "metric": "LUT-GEMM decode GB/s (% HBM peak)",
+            "unit": "GB/s",
+            "peak": PEAK_HBM_GBS,
+            "config": "BASELINE configs[2]: 4-bit codes, k=8192, n=28672, group=128, "
+                      "3 rotating code buffers (>256 MB MALL)",
+            "runs": lut,
+        }
     if not args.no_cpu_baseline:
         from oracle import oracle
         log("[bench] cpu baseline")

@@ -148,6 +148,31 @@ int uor_gfx950_slice_gemm_i8(uint64_t m, uint64_t k, uint64_t n,
  */
 uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n);
 
+/* ============================================ 4-bit table-lookup GEMM */
+
+/*
+ * gemm_tabulated over a TabulatedTriple (crates/uor-matmul-gemm/src/
+ * tabulated.rs:607-658, 2555) with W a CodedMatrix<Packed<Grid<i8,16>,2>>
+ * (crates/uor-matmul-codec/src/codecs.rs:80-259, matrix.rs:36-75):
+ *
+ *   C[i,j] := enc(alpha * sum_p A[i,p] * book_g(j)[code(j,p)] + beta * C[i,j])
+ *
+ * A: m x k int8 view.  codes: n x k/2 bytes, row-major contiguous (one coded
+ * row per output column, k-major); byte q of row j holds k-position 2q in its
+ * LOW nibble and 2q+1 in its high nibble (CK-03).  k must be even and
+ * codes_len == n*k/2 (CodedMatrix::new), else status 3.
+ * books: ceil(n/group) codebooks of 16 int8 entries; coded row j decodes
+ * through book j/group.  The reference spells one codebook per CodedMatrix, so
+ * a per-group codebook is ceil(n/group) reference calls over 128-row
+ * CodedMatrix slices and MatViewMut column windows of C; group == n is one.
+ * c: m x n view of `out_type` elements.  Epilogue and encode as gemm_i8.
+ */
+int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uint64_t codes_len,
+                         uint64_t n, const int8_t *books, uint64_t books_len,
+                         uint64_t group, const uor_view *c, int out_type,
+                         int64_t alpha, int64_t beta, int encode, void *scratch,
+                         uint64_t scratch_bytes, void *stream, uor_route *route);
+
 #ifdef __cplusplus
 }
 #endif

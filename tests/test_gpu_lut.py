@@ -1,0 +1,109 @@
+"""GPU parity of the 4-bit table-lookup GEMM (uor_gfx950_gemm_lut4) against the
+oracle; full decode shapes (m in {1, 8, 32}, k = 8192,
+n = 28672, one codebook per 128 coded rows) against a decode in torch plus a
+float64 matmul, exact because every sum is an integer below 2^53."""
+import numpy as np
+import pytest
+import torch
+
+import gen
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def run_case(oracle, uor, dev, m, k, n, group, seed, out=np.int32, alpha=1, beta=0,
+             encode="nearest", a_strides=None, code_offset=0, expect=None):
+    rng = np.random.default_rng(seed)
+    ars, acs = a_strides or (k, 1)
+    alen = 1 + max(0, (m - 1) * abs(ars) + (k - 1) * abs(acs)) if m and k else 0
+    a = rng.integers(-128, 128, alen + 7).astype(np.int8)
+    codes = rng.integers(0, 256, n * k // 2 + code_offset).astype(np.uint8)
+    books = rng.integers(-128, 128, ((n + group - 1) // group) * 16).astype(np.int8)
+    c0 = rng.integers(np.iinfo(out).min // 2, np.iinfo(out).max // 2, m * n).astype(out)
+    want = c0.copy()
+    st = oracle.gemm_lut4(a, m, k, (ars, acs), codes[code_offset:].copy(), n, books, group, want,
+                          (n, 1), alpha=alpha, beta=beta, encode=encode)
+    gc = to_dev(c0, dev)
+    gcodes = to_dev(codes, dev)[code_offset:]
+    ost = {np.int8: "i8", np.int16: "i16", np.int32: "i32", np.int64: "i64"}[out]
+    gst, route = uor.gemm_lut4(to_dev(a, dev), m, k, (ars, acs), gcodes, n, to_dev(books, dev),
+                               group, gc, (n, 1), out=ost, alpha=alpha, beta=beta, encode=encode)
+    torch.cuda.synchronize()
+    assert uor.STATUS.get(gst, gst) == st
+    assert np.array_equal(gc.cpu().numpy(), want), (m, k, n, group, route)
+    if expect:
+        assert route["tile_n"] == expect, route
+    return route
+
+
+@pytest.mark.parametrize("m,k,n,group", [
+    (1, 2, 1, 1), (1, 64, 37, 5), (1, 8192, 300, 128), (2, 512, 70, 16), (3, 8192, 129, 128),
+    (4, 1000, 64, 64), (5, 256, 33, 7), (8, 8192, 96, 128), (17, 640, 65, 32), (32, 2048, 64, 128),
+    (33, 130, 31, 3), (64, 4096, 40, 128)])
+def test_shapes_against_oracle(oracle, uor, dev, m, k, n, group):
+    run_case(oracle, uor, dev, m, k, n, group, seed=m * 7 + k + n)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_unaligned_and_strided(oracle, uor, dev, m):
+    """Odd code offsets and column-strided activations take the gathering
+    loads; the bytes are the same."""
+    k, n = 256, 45
+    run_case(oracle, uor, dev, m, k, n, 4, seed=5 + m, code_offset=3)
+    run_case(oracle, uor, dev, m, k, n, 4, seed=9 + m, a_strides=(1, m + 2))
+
+
+@pytest.mark.parametrize("out", [np.int8, np.int16, np.int32, np.int64])
+@pytest.mark.parametrize("encode", ["nearest", "wrapping"])
+@pytest.mark.parametrize("m", [1, 9])
+def test_epilogue(oracle, uor, dev, out, encode, m):
+    for alpha, beta in [(1, 0), (3, -1), (1 << 40, -(1 << 35))]:
+        run_case(oracle, uor, dev, m, 128, 40, 8, seed=11, out=out, alpha=alpha, beta=beta,
+                 encode=encode)
+
+
+def test_deep_rows_fold_exactly(oracle, uor, dev):
+    """k past one i32 lane's reach (2^17 weights of |w*a| = 2^14) folds into
+    i64: all -128 activations against a codebook of -128 give k * 2^14."""
+    m, n, k = 2, 3, 1 << 18
+    a = torch.full((m * k,), -128, dtype=torch.int8, device=dev)
+    codes = torch.zeros(n * k // 2, dtype=torch.uint8, device=dev)
+    books = torch.full((16,), -128, dtype=torch.int8, device=dev)
+    c = torch.zeros(m * n, dtype=torch.int64, device=dev)
+    st, _ = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, n, c, (n, 1), out="i64")
+    torch.cuda.synchronize()
+    assert st == 0 and c.cpu().tolist() == [k << 14] * (m * n)
+    c32 = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    st, _ = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, n, c32, (n, 1), out="i32")
+    torch.cuda.synchronize()
+    assert st == 0 and c32.cpu().tolist() == [(1 << 31) - 1] * (m * n)
+
+
+def decode_torch(codes, n, k, books, group):
+    c = codes.view(n, k // 2).to(torch.int64)
+    nib = torch.empty((n, k), dtype=torch.int64, device=codes.device)
+    nib[:, 0::2] = c & 15
+    nib[:, 1::2] = c >> 4
+    g = (torch.arange(n, device=codes.device) // group)[:, None]
+    return books.view(-1, 16).to(torch.int64)[g, nib]
+
+
+@pytest.mark.parametrize("m", [1, 8, 32])
+def test_config3_decode_shape(uor, dev, m):
+    """A uniform i8 (salt 6), codes uniform 0..15 two per byte
+    (salt 7), 224 codebooks uniform i8 (salt 8), k = 8192, n = 28672."""
+    k, n, group = 8192, 28672, 128
+    a = to_dev(gen.i8_full(m * k, 6), dev)
+    codes = to_dev(gen.i8_full(n * k // 2, 7).view(np.uint8), dev)
+    books = to_dev(gen.i8_full((n // group) * 16, 8), dev)
+    c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1))
+    torch.cuda.synchronize()
+    assert st == 0
+    W = decode_torch(codes, n, k, books, group).to(torch.float64)
+    want = a.view(m, k).to(torch.float64) @ W.T
+    assert torch.equal(c.view(m, n).to(torch.float64), want), route

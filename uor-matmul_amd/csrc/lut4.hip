@@ -1,0 +1,412 @@
+// 4-bit table-lookup GEMM on gfx950: C = A * W^T with W coded as
+// Packed<Grid<i8,16>,2> and one 16-entry i8 codebook per group of coded rows.
+//
+// Replaces the reference's gemm_tabulated over a TabulatedTriple
+// (crates/uor-matmul-gemm/src/tabulated.rs:607-658, 2555-2745) for the i8
+// element family and the packed 4-bit codec (crates/uor-matmul-codec/src/
+// codecs.rs:80-259; low nibble = even k, CK-03).  The value is the reference's
+// exactly: every product of an i8 activation and an i8 decoded weight is exact
+// in the i32 lanes (|sum| <= k * 2^14 < 2^31 for k < 2^17; deeper rows fold
+// into i64), then Linear{alpha, beta} and the one encode.
+//
+// Decode.  A code dword holds 8 nibbles: byte b's low nibble is weight 2b, its
+// high nibble weight 2b+1.  With the column's codebook in four SGPRs
+// (entries 0-3, 4-7, 8-11, 12-15), v_perm_b32 picks entries 0-7 and 8-15 for
+// four nibbles at once (selector = nibble & 7), and a third v_perm_b32 picks
+// between the two per byte (selector = byte index + 4 * bit 3).  The even
+// weights [w0 w2 w4 w6] and odd weights [w1 w3 w5 w7] come out as two dwords;
+// the activations they meet are permuted into the same order, once.
+//
+// Algorithmic bytes per call: n*k/2 (codes) + m*k (A) + m*n*out (C) + books;
+// the codes dominate at decode shapes, so the kernels are built to stream
+// them: every code byte is read from HBM exactly once.
+
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace uor {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct LutArgs {
+    const int8_t *a;  // element (0,0) of A
+    int64_t ars, acs;
+    const uint8_t *codes;  // coded row j at codes + j * half
+    uint64_t half;         // k / 2
+    const int8_t *books;
+    uint64_t group;
+    uint64_t m, k, n;
+    char *c;  // element (0,0) of C
+    int64_t crs, ccs;
+    int ob;
+    int64_t alpha, beta;
+    int mode;
+    uint32_t sel_mask, sel_base;  // 0x04040404, 0x03020100 (kernel arguments, so they live in SGPRs)
+};
+
+__device__ inline uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+// 8 weights of one code dword through the codebook (q0..q3 = entries 0-3,
+// 4-7, 8-11, 12-15): even = [w0 w2 w4 w6], odd = [w1 w3 w5 w7].
+// v_and_or_b32 with the mask in an SGPR and the base in a VGPR (one SGPR per
+// VALU op on gfx950): (x & m) | c in one instruction
+// (gfx9 VOP3 takes no literal constants, so the compiler would otherwise
+// spend an AND and an OR).
+__device__ inline uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+    return r;
+}
+
+__device__ inline void decode8(uint32_t w, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3,
+                               uint32_t m4, uint32_t id, uint32_t &even, uint32_t &odd) {
+    // Final selector byte i = i + 4 * (nibble bit 3).
+    uint32_t s = w & 0x07070707u;
+    uint32_t lo = perm(q1, q0, s), hi = perm(q3, q2, s);
+    even = perm(hi, lo, and_or(w >> 1, m4, id));
+    s = (w >> 4) & 0x07070707u;
+    lo = perm(q1, q0, s);
+    hi = perm(q3, q2, s);
+    odd = perm(hi, lo, and_or(w >> 5, m4, id));
+}
+
+// Eight activations A[row][k .. k+8) (zero past k_end or for a row past m)
+// as (even, odd) dwords in the decode's order.
+__device__ inline void act8(const LutArgs &L, uint64_t row, uint64_t k, bool fast, uint32_t &even,
+                            uint32_t &odd) {
+    uint32_t x0 = 0, x1 = 0;
+    if (row < L.m && k < L.k) {
+        const int8_t *p = L.a + (int64_t)row * L.ars + (int64_t)k * L.acs;
+        if (fast && k + 8 <= L.k) {
+            const uint2 v = *(const uint2 *)p;
+            x0 = v.x;
+            x1 = v.y;
+        } else {
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const uint32_t byte =
+                    k + b < L.k ? (uint32_t)(uint8_t)p[(int64_t)b * L.acs] : 0u;
+                if (b < 4) x0 |= byte << (8 * b);
+                else x1 |= byte << (8 * (b - 4));
+            }
+        }
+    }
+    even = perm(x1, x0, 0x06040200u);
+    odd = perm(x1, x0, 0x07050301u);
+}
+
+// Sixteen code bytes of coded row j starting at byte `off` of the row (zero
+// past the row's end or for a column past n).
+__device__ inline uint4 codes16(const LutArgs &L, uint64_t j, uint64_t off, bool fast) {
+    if (j >= L.n || off >= L.half) return make_uint4(0, 0, 0, 0);
+    const uint8_t *p = L.codes + j * L.half + off;
+    if (fast && off + 16 <= L.half) return *(const uint4 *)p;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        const uint32_t byte = off + b < L.half ? (uint32_t)p[b] : 0u;
+        if (b < 4) w[0] |= byte << (8 * b);
+        else if (b < 8) w[1] |= byte << (8 * (b - 4));
+        else if (b < 12) w[2] |= byte << (8 * (b - 8));
+        else w[3] |= byte << (8 * (b - 12));
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// The four dwords of coded row j's codebook (entries 0-3, 4-7, 8-11, 12-15).
+__device__ inline void load_book(const LutArgs &L, uint64_t j, bool aligned, uint32_t &q0,
+                                 uint32_t &q1, uint32_t &q2, uint32_t &q3) {
+    const int8_t *b = L.books + (j / L.group) * 16;
+    if (aligned) {
+        const uint32_t *w = (const uint32_t *)b;
+        q0 = w[0]; q1 = w[1]; q2 = w[2]; q3 = w[3];
+        return;
+    }
+    uint32_t q[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t byte = (uint32_t)(uint8_t)b[e] << (8 * (e & 3));
+        if (e < 4) q[0] |= byte;
+        else if (e < 8) q[1] |= byte;
+        else if (e < 12) q[2] |= byte;
+        else q[3] |= byte;
+    }
+    q0 = q[0]; q1 = q[1]; q2 = q[2]; q3 = q[3];
+}
+
+template <int OB>
+__device__ inline void lut_finish(const LutArgs &L, uint64_t row, uint64_t col, int64_t sum) {
+    char *cp = L.c + ((int64_t)row * L.crs + (int64_t)col * L.ccs) * OB;
+    linear_finish<OB, false>(cp, sum, L.alpha, L.beta, L.mode);
+}
+
+__device__ inline void lut_finish_any(const LutArgs &L, uint64_t row, uint64_t col, int64_t sum) {
+    switch (L.ob) {
+    case 1: lut_finish<1>(L, row, col, sum); break;
+    case 2: lut_finish<2>(L, row, col, sum); break;
+    case 4: lut_finish<4>(L, row, col, sum); break;
+    case 8: lut_finish<8>(L, row, col, sum); break;
+    default: lut_finish<16>(L, row, col, sum); break;
+    }
+}
+
+__device__ inline int wave_sum(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ------------------------------------------------ m <= 4: one wave per column
+//
+// A segment of 8192 weights is 64 lanes x 4 chunks x 32 weights; chunk c of
+// lane l covers weights [(64c + l) * 32, +32) of the segment, i.e. code bytes
+// [(64c + l) * 16, +16), so each code load instruction of the wave reads 1 KiB
+// contiguously.  The lane's activations for the segment (MR rows x 128
+// weights) sit in registers, permuted to the decode's order, and are reused
+// for every column the wave visits.
+constexpr int LUT_SEG = 8192;
+
+template <bool FAST>
+__device__ inline uint4 code_chunk(const LutArgs &L, uint64_t j, uint64_t off) {
+    if constexpr (FAST) {
+        // Rows are whole 16-byte chunks (k/2 % 16 == 0, 16-byte aligned).
+        if (j < L.n && off < L.half) return *(const uint4 *)(L.codes + j * L.half + off);
+        return make_uint4(0, 0, 0, 0);
+    } else {
+        return codes16(L, j, off, false);
+    }
+}
+
+template <int MR, bool FAST>
+__global__ void __launch_bounds__(256) lut4_dot4_kernel(LutArgs L, int book_aligned) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t wave = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint64_t nwaves = ((uint64_t)gridDim.x * blockDim.x) >> 6;
+    const bool segs1 = L.k <= (uint64_t)LUT_SEG;
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+
+    uint32_t ae[MR][4][4], ao[MR][4][4];
+    auto load_act = [&](uint64_t k0) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    act8(L, r, k0 + (uint64_t)(64 * c + lane) * 32 + 8 * d, FAST, ae[r][c][d], ao[r][c][d]);
+    };
+    if (segs1) load_act(0);
+
+    // Two columns per pass, j and j + nwaves: their decodes and their wave
+    // reductions are independent, so each hides the other's latency.
+    for (uint64_t j = wave; j < L.n; j += 2 * nwaves) {
+        const uint64_t jj[2] = {j, j + nwaves};
+        uint32_t q[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint64_t ju = jj[u] < L.n ? jj[u] : j;
+            load_book(L, ju, book_aligned, q[u][0], q[u][1], q[u][2], q[u][3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[u][e] = __builtin_amdgcn_readfirstlane(q[u][e]);
+        }
+        int acc[2][MR];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < MR; ++r) acc[u][r] = 0;
+        for (uint64_t k0 = 0; k0 < L.k; k0 += LUT_SEG) {
+            if (!segs1) load_act(k0);
+            uint4 cw[2][4];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    cw[u][c] = code_chunk<FAST>(L, jj[u], k0 / 2 + (uint64_t)(64 * c + lane) * 16);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const uint32_t w = d == 0 ? cw[u][c].x : d == 1 ? cw[u][c].y : d == 2 ? cw[u][c].z : cw[u][c].w;
+                        uint32_t e, o;
+                        decode8(w, q[u][0], q[u][1], q[u][2], q[u][3], m4, id, e, o);
+#pragma unroll
+                        for (int r = 0; r < MR; ++r) {
+                            acc[u][r] = __builtin_amdgcn_sdot4((int)e, (int)ae[r][c][d], acc[u][r], false);
+                            acc[u][r] = __builtin_amdgcn_sdot4((int)o, (int)ao[r][c][d], acc[u][r], false);
+                        }
+                    }
+                }
+            }
+        }
+        // (k <= 65536 here: the host sends deeper rows to the MFMA kernel,
+        // whose partial sums fold into i64.)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            int s0 = acc[0][r], s1 = acc[1][r];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                s0 += __shfl_xor(s0, o, 64);
+                s1 += __shfl_xor(s1, o, 64);
+            }
+            if (lane == r && (uint64_t)r < L.m) lut_finish_any(L, r, jj[0], s0);
+            if (lane == 32 + r && (uint64_t)r < L.m && jj[1] < L.n) lut_finish_any(L, r, jj[1], s1);
+        }
+    }
+}
+
+// --------------------------------------- m > 4: decoded weights into MFMA
+//
+// A workgroup of 4 waves owns a 32-row x 32-column output tile; wave w sums
+// the w-th quarter of k.  Lane l handles coded row (column) j0 + l%32 and
+// half h = l/32 of each 128-weight step: its 32 code bytes cover weights
+// [64h, 64h+64) of the step and decode into four MFMA B operands; the
+// matching A operands are 16 activations each, permuted the same way.  The
+// four quarters meet in LDS as exact i64 sums.
+__global__ void __launch_bounds__(256) lut4_mfma_kernel(LutArgs L, int fast, int book_aligned, uint64_t kq) {
+    __shared__ long long red[4][32 * 33];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int jl = lane & 31, h = lane >> 5;
+    const uint64_t ntile = (L.n + 31) / 32;
+    const uint64_t col_tile = blockIdx.x % ntile, row_tile = blockIdx.x / ntile;
+    const uint64_t j0 = col_tile * 32, r0 = row_tile * 32;
+    const uint64_t j = j0 + jl;
+    const uint64_t kbeg = (uint64_t)wave * kq;
+    const uint64_t kend = min(L.k, kbeg + kq);
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+
+    uint32_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    if (j < L.n) load_book(L, j, book_aligned, q0, q1, q2, q3);
+    v16i acc = v16i{};
+    long long wide[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wide[r] = 0;
+    uint64_t since_fold = 0;
+
+    for (uint64_t k0 = kbeg; k0 < kend; k0 += 128) {
+        const uint64_t kb = k0 + 64 * h;  // this lane's 64 weights
+        const uint4 c0 = codes16(L, j, kb / 2, fast);
+        const uint4 c1 = codes16(L, j, kb / 2 + 16, fast);
+        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t e0, o0, e1, o1;
+            decode8(cw[2 * t], q0, q1, q2, q3, m4, id, e0, o0);
+            decode8(cw[2 * t + 1], q0, q1, q2, q3, m4, id, e1, o1);
+            // Quarters are whole 128-weight steps, so only the last step of
+            // the row can run past k: there the codes read as zero bytes
+            // (book[0]) and act8 gives zero activations, so those products
+            // vanish.
+            const uint64_t ka = kb + 16 * t;
+            uint32_t ae0, ao0, ae1, ao1;
+            act8(L, r0 + jl, ka, fast, ae0, ao0);
+            act8(L, r0 + jl, ka + 8, fast, ae1, ao1);
+            const v4i bop = v4i{(int)e0, (int)o0, (int)e1, (int)o1};
+            const v4i aop = v4i{(int)ae0, (int)ao0, (int)ae1, (int)ao1};
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, acc, 0, 0, 0);
+        }
+        since_fold += 128;
+        if (since_fold >= 65536) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) wide[r] += acc[r];
+            acc = v16i{};
+            since_fold = 0;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        wide[r] += acc[r];
+        red[wave][(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + jl] = wide[r];
+    }
+    __syncthreads();
+    // 1024 cells, 256 threads: four each.
+    for (int q = threadIdx.x; q < 1024; q += 256) {
+        const int row = q >> 5, col = q & 31;
+        const long long s = red[0][row * 33 + col] + red[1][row * 33 + col] +
+                            red[2][row * 33 + col] + red[3][row * 33 + col];
+        if (r0 + row < L.m && j0 + col < L.n) lut_finish_any(L, r0 + row, j0 + col, (int64_t)s);
+    }
+}
+
+}  // namespace uor
+
+using namespace uor;
+
+extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uint64_t codes_len,
+                                    uint64_t n, const int8_t *books, uint64_t books_len,
+                                    uint64_t group, const uor_view *c, int out_type, int64_t alpha,
+                                    int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
+                                    void *stream, uor_route *route) {
+    (void)scratch;
+    (void)scratch_bytes;
+    route_set(route, UOR_ROUTE_NONE);
+    if (!valid_out_type(out_type) || !valid_encode(encode)) return UOR_INVALID_ARGUMENT;
+    if (!a || !c) return UOR_INVALID_ARGUMENT;
+    Placed A, C;
+    int st;
+    if ((st = place(a, 1, &A))) return st;
+    const uint64_t m = A.rows, k = A.cols;
+    // CodedMatrix::new (matrix.rs:36-75): a fixed-width tier of MAX_BLOCK 2
+    // needs an even row width and exactly n * k/2 codes.
+    if (k % 2 != 0) return UOR_SHORT_BUFFER;
+    uint64_t need;
+    if (__builtin_mul_overflow(n, k / 2, &need) || need != codes_len) return UOR_SHORT_BUFFER;
+    if (group == 0) return UOR_INVALID_ARGUMENT;
+    const uint64_t ngroups = n == 0 ? 0 : (n + group - 1) / group;
+    if (books_len < ngroups * 16) return UOR_SHORT_BUFFER;
+    if (n > 0 && need > 0 && !codes) return UOR_SHORT_BUFFER;
+    if (ngroups > 0 && !books) return UOR_SHORT_BUFFER;
+    if ((st = place(c, out_type, &C))) return st;
+    // TabulatedTriple::new (tabulated.rs:628-658).
+    if (C.rows != m || C.cols != n) return UOR_NONCONFORMANT;
+    if (self_aliases(C.rows, C.cols, C.rs, C.cs)) return UOR_OUTPUT_ALIASES_ITSELF;
+    if (m == 0 || n == 0) return UOR_OK;
+
+    LutArgs L{(const int8_t *)A.base, A.rs, A.cs, codes, k / 2, books, group, m, k, n,
+              C.base, C.rs, C.cs, out_type, alpha, beta, encode, 0x04040404u, 0x03020100u};
+    hipStream_t s = (hipStream_t)stream;
+    // 16-byte code loads need 16-byte aligned rows; 8-byte activation loads
+    // need a unit column stride and 8-byte aligned rows.
+    const bool code_fast = ((uintptr_t)codes % 16 == 0) && ((k / 2) % 16 == 0);
+    const bool act_fast = A.cs == 1 && ((uintptr_t)A.base % 8 == 0) && (A.rs % 8 == 0 || m == 1);
+    const int fast = code_fast && act_fast;
+    const int book_aligned = (uintptr_t)books % 4 == 0;
+    if (route) {
+        route->kind = UOR_ROUTE_LUT4_DOT4;
+        route->launches = 1;
+        route->operand_modes = fast;
+    }
+    if (m <= 4 && k <= 65536) {
+        // 4096 persistent waves (four per SIMD), each walking columns j,
+        // j + W, ...: a sweep of 2048..14336 on MI355X put the optimum here.
+        const uint64_t waves = n < 4096 ? n : 4096;
+        const unsigned blocks = (unsigned)((waves + 3) / 4);
+        if (route) route->tile_m = m <= 1 ? 1 : m <= 2 ? 2 : 4, route->tile_n = 1;
+        if (fast) {
+            if (m <= 1) hipLaunchKernelGGL((lut4_dot4_kernel<1, true>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
+            else if (m <= 2) hipLaunchKernelGGL((lut4_dot4_kernel<2, true>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
+            else hipLaunchKernelGGL((lut4_dot4_kernel<4, true>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
+        } else {
+            if (m <= 1) hipLaunchKernelGGL((lut4_dot4_kernel<1, false>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
+            else if (m <= 2) hipLaunchKernelGGL((lut4_dot4_kernel<2, false>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
+            else hipLaunchKernelGGL((lut4_dot4_kernel<4, false>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
+        }
+        UOR_HIP(hipGetLastError());
+        return UOR_OK;
+    }
+    // Quarter of k per wave, in whole 128-weight steps.
+    uint64_t kq = (k + 3) / 4;
+    kq = (kq + 127) / 128 * 128;
+    if (kq == 0) kq = 128;
+    const uint64_t tiles = ((n + 31) / 32) * ((m + 31) / 32);
+    if (route) route->tile_m = 32, route->tile_n = 32, route->split_k = 4;
+    if (tiles > 0x7FFFFFFFull) return UOR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(lut4_mfma_kernel, dim3((unsigned)tiles), dim3(256), 0, s, L, fast, book_aligned, kq);
+    UOR_HIP(hipGetLastError());
+    return UOR_OK;
+}
