@@ -39,6 +39,7 @@ sys.path.insert(0, str(ROOT / "tests"))
 METRIC = "exact i8 GEMM TOPS @8192³ (% MFMA peak); LUT-GEMM decode GB/s (% HBM peak)"
 PEAK_INT8_TOPS = 5000.0  # dense int8 MFMA, MI355X (5.0 POP/s)
 PEAK_HBM_GBS = 8000.0    # HBM3E
+PEAK_TROP_TERMS = 256 * 64 * 2.4e9  # packed-i16 VALU (+, max) terms/s
 
 
 def log(msg):
@@ -183,6 +184,53 @@ def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
     return out
 
 
+def bench_trop(args, torch, uor, gen):
+    """Trop<i8> max-plus GEMM at m = n = k = 4096, 5% of entries
+    at the semiring zero, output Trop<i32>.  One term is one (+, max) pair;
+    the packed-i16 VALU ceiling is 256 CUs x 64 lanes x 2.4 GHz = 39.3e12
+    terms/s (v_pk_add_u16 and v_pk_max_i16 each cover two terms)."""
+    import numpy as np
+    N = 4096
+    dev = torch.device("cuda:0")
+    rec = np.dtype([("value", "i1"), ("finite", "u1")])
+
+    def recs(salt):
+        v = gen.i8_full(N * N, salt)
+        f = (gen.lanes_draws(N * N, 100 + salt) % np.uint64(20)) != 0
+        r = np.zeros(N * N, rec)
+        r["value"] = np.where(f, v, 0)
+        r["finite"] = f
+        return torch.from_numpy(r.view(np.uint8)).to(dev)
+
+    a, b = recs(11), recs(12)
+    c = torch.zeros(N * N * 8, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        st, _ = uor.gemm_trop_i8(a, (N, N), (N, 1), b, (N, N), (N, 1), c, (N, N), (N, 1),
+                                 stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"trop status {st}")
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    steps = max(args.steps, 10)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(steps):
+        step()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    ms = s0.elapsed_time(s1) / steps
+    terms = float(N) ** 3
+    rate = terms / (ms * 1e-3)
+    return {"m": N, "n": N, "k": N, "out": "Trop<i32>", "ms_per_call": round(ms, 5),
+            "terms_per_s": round(rate / 1e12, 3), "unit": "Tterm/s",
+            "peak": PEAK_TROP_TERMS / 1e12, "frac_valu": round(rate / PEAK_TROP_TERMS, 4),
+            "kernel": "trop_i8_kernel", "bound": "valu"}
+
+
 def cpu_baseline_i8(host, oracle):
     """The reference's packed route restated (oracle/fastroute.cpp) on a row
     slab of the same 8192^3 problem, all usable host cores."""
@@ -226,6 +274,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-lut", action="store_true", help="skip the secondary LUT decode figure")
+    ap.add_argument("--no-trop", action="store_true", help="skip the secondary max-plus figure")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device-to-device copy and exit (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -258,6 +307,13 @@ def main():
             "config": "BASELINE configs[2]: 4-bit codes, k=8192, n=28672, group=128, "
                       "3 rotating code buffers (>256 MB MALL)",
             "runs": lut,
+        }
+    if not args.no_trop:
+        log("[bench] trop max-plus")
+        result["tropical"] = {
+            "metric": "Trop<i8> max-plus terms/s (% packed-i16 VALU peak)",
+            "config": "BASELINE configs[4]: m=n=k=4096, 5% -inf entries, Trop<i32> output",
+            "run": bench_trop(args, torch, uor, gen),
         }
     if not args.no_cpu_baseline:
         from oracle import oracle

@@ -173,6 +173,29 @@ int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uint64_t codes
                          int64_t alpha, int64_t beta, int encode, void *scratch,
                          uint64_t scratch_bytes, void *stream, uor_route *route);
 
+/* ================================================ (max, +) over Trop<i8> */
+
+/*
+ * gemm(&mut Triple, &MaxPlus{alpha,beta}, GemmOptions{encode}, ..) at
+ * E = Trop<i8>, O = Trop<out> (the reference traversal driver::gemm,
+ * crates/uor-matmul-gemm/src/driver.rs:67-182, the public route for Trop):
+ *
+ *   C[i,j] := enc((alpha (x) max_p (A[i,p] + B[p,j])) (+) (beta (x) C[i,j]))
+ *
+ * over finite pairs only; -inf absorbs (tropical.rs:311-318).
+ * a, b: views of 2-byte Trop<i8> records {int8 value; uint8 finite}
+ * (#[repr(C)], tropical.rs:63-70).  c: view of Trop<O> records {O value;
+ * uint8 finite; padding}, O = out_type in {1,2,4,8} bytes, record size
+ * 2*out_type.  Finite values encode through [O::MIN+1, O::MAX-1]
+ * (tropical.rs:336-350); -inf writes {0, 0}.  alpha/beta are Trop<i64>
+ * (value, finite); beta = -inf never reads C (CS-11).
+ */
+int uor_gfx950_gemm_trop_i8(const uor_view *a, const uor_view *b, const uor_view *c,
+                            int out_type, int64_t alpha, int alpha_finite,
+                            int64_t beta, int beta_finite, int encode,
+                            void *scratch, uint64_t scratch_bytes, void *stream,
+                            uor_route *route);
+
 #ifdef __cplusplus
 }
 #endif

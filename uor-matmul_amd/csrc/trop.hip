@@ -1,0 +1,209 @@
+// (max, +) GEMM over Trop<i8> on gfx950 VALU.
+//
+// Replaces the reference's public tropical route, driver::gemm at
+// E = Trop<i8> with the MaxPlus epilogue (crates/uor-matmul-gemm/src/
+// driver.rs:67-182, epilogue.rs:137-192), whose fastest CPU sequence is the
+// packed saturating-i16 TROP_I16 / AVX2_TROP_I16 (crates/uor-matmul-kernels/
+// src/tropical.rs:91-166, isa/x86.rs:935-1055).  A max-plus product is not a
+// contraction, so there is no MFMA form; it runs on packed 16-bit VALU.
+//
+// Exactness.  Each Trop<i8> operand becomes an i16: its value when finite,
+// NEG (-16384) at the semiring zero.  A finite sum lies in [-256, 254]; a sum
+// touching NEG lies in [-16512, -16257], and NEG + NEG = -32768 exactly, so
+// plain 16-bit adds never wrap.  The max over k of the sums is therefore the
+// exact TropAcc value when some pair is finite, and below -256 exactly when
+// every pair touched -inf (tropical.rs:311-318: -inf absorbs).  No depth term
+// enters: a max does not grow with k (trop_acc_bits, tropical.rs:289).
+//
+// Data path.  A 128 x 128 output tile per workgroup of 256 threads, 8 x 8
+// cells per thread.  Each k-step of 32 stages A as [row][k] and B as
+// [column][k] i16 in LDS; a thread reads eight consecutive k of its rows and
+// columns with ds_read_b128 and runs v_pk_add_u16 + v_pk_max_i16 on (k, k+1)
+// pairs, so one VALU instruction covers one term and the two halves of each
+// cell's accumulator are maxed at the end.
+
+#include "common.hpp"
+
+namespace uor {
+
+typedef short s2 __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int TB = 128;     // tile edge
+constexpr int TK = 32;      // k per stage
+constexpr int TSTR = TK + 8; // LDS row stride in i16 (80 bytes: conflict-free b128 reads)
+constexpr short NEG = -16384;
+
+struct TropArgs {
+    const uint8_t *a;  // record (0,0) of A; records are 2 bytes
+    int64_t ars, acs;
+    const uint8_t *b;
+    int64_t brs, bcs;
+    uint64_t m, k, n;
+    uint8_t *c;  // record (0,0) of C; records are 2*ob bytes
+    int64_t crs, ccs;
+    int ob;
+    int64_t alpha;
+    int alpha_finite;
+    int64_t beta;
+    int beta_finite;
+    int mode;
+};
+
+__device__ inline short trop16(const uint8_t *rec) {
+    const uint16_t r = *(const uint16_t *)rec;  // {value, finite}
+    return (r >> 8) ? (short)(int8_t)(r & 0xFF) : NEG;
+}
+
+// encode_i128_into over [O::MIN + 1, O::MAX - 1] (tropical.rs:336-350).
+__device__ inline i128 trop_encode(i128 v, int bytes, int mode) {
+    i128 mn, mx;
+    out_range(bytes, &mn, &mx);
+    mn += 1;
+    mx -= 1;
+    if (v >= mn && v <= mx) return v;
+    if (mode != UOR_ENCODE_WRAPPING) return v < mn ? mn : mx;
+    const u128 span = (u128)mx - (u128)mn + 1;
+    const u128 off = (u128)v - (u128)mn;
+    return (i128)(off % span + (u128)mn);
+}
+
+template <int OB>
+__device__ inline void trop_store(uint8_t *p, bool finite, i128 v) {
+    store_out<OB>((char *)p, finite ? v : 0);
+    p[OB] = finite ? 1 : 0;
+}
+
+template <int OB>
+__device__ inline void trop_finish(const TropArgs &T, uint64_t i, uint64_t j, int acc) {
+    // MaxPlus::finish (epilogue.rs:159-192): (alpha (x) P) (+) (beta (x) C).
+    uint8_t *cp = T.c + ((int64_t)i * T.crs + (int64_t)j * T.ccs) * (2 * OB);
+    bool fin = acc >= -256 && T.alpha_finite;
+    i128 total = fin ? (i128)acc + T.alpha : 0;
+    if (T.beta_finite) {
+        const bool cf = cp[OB] != 0;
+        if (cf) {
+            const i128 prior = load_out<OB>((const char *)cp) + (i128)T.beta;
+            if (!fin || prior > total) total = prior;
+            fin = true;
+        }
+    }
+    if (fin) trop_store<OB>(cp, true, trop_encode(total, OB, T.mode));
+    else trop_store<OB>(cp, false, 0);
+}
+
+__global__ void __launch_bounds__(256) trop_i8_kernel(TropArgs T, int gm, int gn) {
+    __shared__ __attribute__((aligned(16))) short As[TB * TSTR];
+    __shared__ __attribute__((aligned(16))) short Bs[TB * TSTR];
+    const int t = threadIdx.x;
+    const int ty = t >> 4, tx = t & 15;
+    const uint64_t tm = blockIdx.x / gn, tn = blockIdx.x % gn;
+    const uint64_t m0 = tm * TB, n0 = tn * TB;
+
+    s2 acc[8][8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[a][b] = s2{-32768, -32768};
+
+    for (uint64_t k0 = 0; k0 < T.k; k0 += TK) {
+        // A tile: 128 rows x 32 k; consecutive threads walk k.
+#pragma unroll 4
+        for (int q = 0; q < 16; ++q) {
+            const int p = t & 31, r = (t >> 5) + 8 * q;
+            const uint64_t gi = m0 + r, gk = k0 + p;
+            As[r * TSTR + p] = (gi < T.m && gk < T.k)
+                                   ? trop16(T.a + ((int64_t)gi * T.ars + (int64_t)gk * T.acs) * 2)
+                                   : NEG;
+        }
+        // B tile: 32 k x 128 columns, stored [column][k]; consecutive threads
+        // walk columns.
+#pragma unroll 4
+        for (int q = 0; q < 16; ++q) {
+            const int col = t & 127, p = (t >> 7) + 2 * q;
+            const uint64_t gj = n0 + col, gk = k0 + p;
+            Bs[col * TSTR + p] = (gj < T.n && gk < T.k)
+                                     ? trop16(T.b + ((int64_t)gk * T.brs + (int64_t)gj * T.bcs) * 2)
+                                     : NEG;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p0 = 0; p0 < TK; p0 += 8) {
+            v4i av[8], bv[8];
+#pragma unroll
+            for (int a = 0; a < 8; ++a) av[a] = *(const v4i *)(As + (ty + 16 * a) * TSTR + p0);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) bv[b] = *(const v4i *)(Bs + (tx + 16 * b) * TSTR + p0);
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int a = 0; a < 8; ++a)
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) {
+                        // Copy the lanes out before the cast: a bit_cast of a
+                        // vector-subscript lvalue reads element 0 under this
+                        // compiler, whatever the subscript.
+                        const int xa = av[a][d], yb = bv[b][d];
+                        const s2 x = __builtin_bit_cast(s2, xa);
+                        const s2 y = __builtin_bit_cast(s2, yb);
+                        acc[a][b] = __builtin_elementwise_max(acc[a][b], x + y);
+                    }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        const uint64_t i = m0 + ty + 16 * a;
+        if (i >= T.m) continue;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint64_t j = n0 + tx + 16 * b;
+            if (j >= T.n) continue;
+            const int v = acc[a][b][0] > acc[a][b][1] ? acc[a][b][0] : acc[a][b][1];
+            switch (T.ob) {
+            case 1: trop_finish<1>(T, i, j, v); break;
+            case 2: trop_finish<2>(T, i, j, v); break;
+            case 4: trop_finish<4>(T, i, j, v); break;
+            default: trop_finish<8>(T, i, j, v); break;
+            }
+        }
+    }
+}
+
+}  // namespace uor
+
+using namespace uor;
+
+extern "C" int uor_gfx950_gemm_trop_i8(const uor_view *a, const uor_view *b, const uor_view *c,
+                                       int out_type, int64_t alpha, int alpha_finite, int64_t beta,
+                                       int beta_finite, int encode, void *scratch,
+                                       uint64_t scratch_bytes, void *stream, uor_route *route) {
+    (void)scratch;
+    (void)scratch_bytes;
+    route_set(route, UOR_ROUTE_NONE);
+    if (!(out_type == 1 || out_type == 2 || out_type == 4 || out_type == 8)) return UOR_INVALID_ARGUMENT;
+    if (!valid_encode(encode)) return UOR_INVALID_ARGUMENT;
+    Placed A, B, C;
+    // Records: Trop<i8> is 2 bytes; Trop<O> is 2 * sizeof(O).
+    int st = make_triple(a, 2, b, 2, c, 2 * out_type, &A, &B, &C);
+    if (st) return st;
+    if (C.rows == 0 || C.cols == 0) return UOR_OK;
+    if (((uintptr_t)A.base | (uintptr_t)B.base) & 1) return UOR_INVALID_ARGUMENT;
+    TropArgs T{(const uint8_t *)A.base, A.rs, A.cs, (const uint8_t *)B.base, B.rs, B.cs,
+               A.rows, A.cols, B.cols, (uint8_t *)C.base, C.rs, C.cs, out_type,
+               alpha, alpha_finite != 0, beta, beta_finite != 0, encode};
+    const uint64_t gm = (T.m + TB - 1) / TB, gn = (T.n + TB - 1) / TB;
+    if (gm * gn > 0x7FFFFFFFull) return UOR_INVALID_ARGUMENT;
+    if (route) {
+        route->kind = UOR_ROUTE_TROP_VALU;
+        route->tile_m = route->tile_n = TB;
+        route->tile_k = TK;
+        route->split_k = 1;
+        route->launches = 1;
+    }
+    hipLaunchKernelGGL(trop_i8_kernel, dim3((unsigned)(gm * gn)), dim3(256), 0, (hipStream_t)stream,
+                       T, (int)gm, (int)gn);
+    UOR_HIP(hipGetLastError());
+    return UOR_OK;
+}
