@@ -173,6 +173,57 @@ int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uint64_t codes
                          int64_t alpha, int64_t beta, int encode, void *scratch,
                          uint64_t scratch_bytes, void *stream, uor_route *route);
 
+/* =================================================== exact float GEMM */
+
+/*
+ * gemm_float_packed through the view API (crates/uor-matmul-gemm/src/
+ * float.rs:1824-1855), E = O = f32 (is_f64 = 0) or f64 (is_f64 = 1):
+ *
+ *   C := round_once(alpha * sum_p A[i,p]*B[p,j] + beta * C[i,j])
+ *
+ * computed exactly (Element::mac for floats, crates/uor-matmul-core/src/
+ * alphabet.rs:856-902; Complete::scale, acc.rs:1028; Linear::finish) and
+ * rounded once by the float encode (acc.rs:1734-1868): Nearest is
+ * round-half-even with overflow to +-inf; the other modes truncate toward
+ * zero and clamp to +-MAX.  An exact zero gives +0; NaN anywhere, inf*0 or
+ * +inf with -inf give the canonical NaN.  alpha and beta are exact int64.
+ */
+int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_view *b,
+                          const uor_view *c, int64_t alpha, int64_t beta, int encode,
+                          void *scratch, uint64_t scratch_bytes, void *stream,
+                          uor_route *route);
+
+/* slice::gemm_float_ex (crates/uor-matmul/src/slice.rs:304-340), encode
+ * Nearest, row-major with leading dimensions. */
+int uor_gfx950_slice_gemm_float_ex(int is_f64, uint64_t m, uint64_t k, uint64_t n,
+                                   int64_t alpha, const void *a, uint64_t a_len,
+                                   uint64_t lda, const void *b, uint64_t b_len,
+                                   uint64_t ldb, int64_t beta, void *c, uint64_t c_len,
+                                   uint64_t ldc, void *scratch, uint64_t scratch_bytes,
+                                   void *stream);
+
+/*
+ * raw::sgemm / raw::dgemm (crates/uor-matmul/src/raw.rs:45-90, raw_gemm
+ * :98-158): matrixmultiply's signature.  a, b, c point at element (0,0);
+ * strides may be negative.  Like the reference, an invalid request is a silent
+ * no-op (status 0, nothing enqueued); a HIP failure still reports 100+.
+ */
+int uor_gfx950_sgemm(uint64_t m, uint64_t k, uint64_t n, int64_t alpha,
+                     const float *a, int64_t rsa, int64_t csa,
+                     const float *b, int64_t rsb, int64_t csb, int64_t beta,
+                     float *c, int64_t rsc, int64_t csc, void *scratch,
+                     uint64_t scratch_bytes, void *stream);
+int uor_gfx950_dgemm(uint64_t m, uint64_t k, uint64_t n, int64_t alpha,
+                     const double *a, int64_t rsa, int64_t csa,
+                     const double *b, int64_t rsb, int64_t csb, int64_t beta,
+                     double *c, int64_t rsc, int64_t csc, void *scratch,
+                     uint64_t scratch_bytes, void *stream);
+
+/* The offer that lets gemm_float take its fastest route at this shape
+ * (replaces suggested_float_panels, float.rs:1876-1882, for this backend). */
+uint64_t uor_gfx950_suggested_scratch_float(int is_f64, uint64_t m, uint64_t k,
+                                            uint64_t n);
+
 /* ================================================ (max, +) over Trop<i8> */
 
 /*

@@ -1,0 +1,198 @@
+"""GPU parity of the exact float GEMM (uor_gfx950_gemm_float and its slice /
+raw faces) against the oracle, bit for bit: the reference's float corpus in
+every encode mode, alpha/beta with non-finite priors, the raw face's stride
+matrix and degenerate extents (raw.rs:167-311), and BASELINE configs[3]
+distributions at reduced sizes."""
+import numpy as np
+import pytest
+import torch
+
+import gen
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
+
+MODES = ["nearest", "toward_zero", "saturating", "wrapping"]
+
+
+def bits(x):
+    return x.view(np.uint64 if x.dtype == np.float64 else np.uint32)
+
+
+def check(oracle, uor, dev, a, b, m, k, n, c0=None, alpha=1, beta=0, mode="nearest",
+          a_strides=None, c_strides=None, scratch=None, expect_route=None):
+    ars = a_strides or (k, 1)
+    crs = c_strides or (n, 1)
+    c0 = np.zeros(m * n, a.dtype) if c0 is None else c0
+    want = c0.copy()
+    st = oracle.gemm_float(a, (m, k), ars, b, (k, n), (n, 1), want, (m, n), crs, alpha=alpha,
+                           beta=beta, encode=mode)
+    gc = torch.from_numpy(c0.copy()).to(dev)
+    gst, route = uor.gemm_float(torch.from_numpy(a).to(dev), (m, k), ars,
+                                torch.from_numpy(b).to(dev), (k, n), (n, 1), gc, (m, n), crs,
+                                alpha=alpha, beta=beta, encode=mode, scratch=scratch)
+    torch.cuda.synchronize()
+    assert uor.STATUS.get(gst, gst) == st
+    got = gc.cpu().numpy()
+    if not np.array_equal(bits(got), bits(want)):
+        bad = np.nonzero(bits(got) != bits(want))[0][:5]
+        raise AssertionError(f"{m}x{k}x{n} {mode} a={alpha} b={beta} route={route}: cells {bad.tolist()} "
+                             f"got {got[bad].tolist()} want {want[bad].tolist()}")
+    if expect_route:
+        assert route["kind"] == expect_route, route
+    return route
+
+
+@pytest.mark.parametrize("is64", [False, True])
+@pytest.mark.parametrize("case", gen.CORRECTNESS_CASES + gen.PERFORMANCE_CASES,
+                         ids=lambda c: f"{c[3]}-{c[4]}")
+def test_corpus(oracle, uor, dev, is64, case):
+    m, k, n = case[:3]
+    a, b = gen.corpus_operands(case, is64)
+    modes = MODES if m * k * n <= 4096 else ["nearest", "toward_zero"]
+    for mode in modes:
+        check(oracle, uor, dev, a, b, m, k, n, mode=mode)
+
+
+@pytest.mark.parametrize("is64", [False, True])
+def test_alpha_beta(oracle, uor, dev, is64):
+    ft = np.float64 if is64 else np.float32
+    rng = np.random.default_rng(11 + is64)
+    m, k, n = 9, 40, 11
+    a, b = gen.corpus_operands((m, k, n, "FewGrades", 41), is64)
+    c0 = (rng.standard_normal(m * n) * 2.0 ** rng.integers(-60, 60, m * n)).astype(ft)
+    c0[[3, 7, 11, 12, 50]] = [np.inf, -np.inf, np.nan, 0.0, -0.0]
+    for alpha, beta in [(1, 1), (3, -1), (0, 2), (-7, 0), (1 << 40, -(1 << 50)), (0, 0),
+                        (-(1 << 63), 1), ((1 << 63) - 1, -(1 << 63))]:
+        for mode in ("nearest", "toward_zero"):
+            check(oracle, uor, dev, a, b, m, k, n, c0=c0, alpha=alpha, beta=beta, mode=mode)
+
+
+@pytest.mark.parametrize("is64", [False, True])
+def test_nonfinite_rows_and_columns(oracle, uor, dev, is64):
+    ft = np.float64 if is64 else np.float32
+    m, k, n = 6, 50, 7
+    a, b = gen.corpus_operands((m, k, n, "FullFiniteRange", 5), is64)
+    a = a.copy()
+    b = b.copy()
+    a[1 * k + 3] = np.inf          # row 1: inf against B[3, :]
+    b[3 * n + 2] = 0.0             # ... which is NaN at column 2
+    a[2 * k + 4] = -np.inf
+    b[10 * n + 5] = np.nan         # column 5 is NaN everywhere
+    a[4 * k + 7] = np.inf
+    a[4 * k + 8] = -np.inf         # row 4: +inf and -inf -> NaN
+    for mode in MODES:
+        check(oracle, uor, dev, a, b, m, k, n, mode=mode)
+    check(oracle, uor, dev, a, b, m, k, n, alpha=0)
+    check(oracle, uor, dev, a, b, m, k, n, alpha=-2, beta=1, c0=np.full(m * n, ft(1.5)))
+
+
+def strided(rs, cs, rows, cols, f, ft):
+    """raw.rs Strided::new: the window the strides reach, NaN elsewhere, and
+    the offset of element (0, 0)."""
+    offs = [i * rs + j * cs for i in range(rows) for j in range(cols)]
+    lo = min(offs) if offs else 0
+    span = (max(offs) - lo + 1) if offs else 0
+    buf = np.full(span, np.nan, ft)
+    for i in range(rows):
+        for j in range(cols):
+            buf[i * rs + j * cs - lo] = f(i, j)
+    return buf, -lo
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 7, 5), (4, 16, 6), (13, 17, 19)])
+def test_raw_stride_matrix(oracle, uor, dev, shape):
+    """raw.rs:167-241: seven A stride pairs by three C stride pairs."""
+    m, k, n = shape
+    ft = np.float32
+    checked = 0
+    for rsa, csa in [(k, 1), (1, m), (-k, 1), (k, -1), (-k, -1), (2 * k, 2), (-2 * k, 2)]:
+        for rsc, csc in [(n, 1), (-n, 1), (n, -1)]:
+            abuf, aoff = strided(rsa, csa, m, k, lambda i, j: (i * k + j) * 0.5 - 3.0, ft)
+            bbuf, boff = strided(n, 1, k, n, lambda i, j: (i * n + j) * -0.25 + 1.5, ft)
+            cbuf, coff = strided(rsc, csc, m, n, lambda i, j: 0.0, ft)
+            want = cbuf.copy()
+            # The oracle takes buffer-start views; the raw face takes (0,0).
+            st = oracle.gemm_float(abuf, (m, k), (rsa, csa), bbuf, (k, n), (n, 1), want, (m, n),
+                                   (rsc, csc))
+            assert st == "ok"
+            ga, gb = torch.from_numpy(abuf).to(dev), torch.from_numpy(bbuf).to(dev)
+            gc = torch.from_numpy(cbuf.copy()).to(dev)
+            assert uor.raw_gemm(m, k, n, 1, ga, rsa, csa, gb, n, 1, 0, gc, rsc, csc, a_off=aoff,
+                                b_off=boff, c_off=coff) == 0
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(gc.cpu().numpy()), bits(want)), (rsa, csa, rsc, csc)
+            checked += 1
+    assert checked == 21
+
+
+def test_raw_degenerate_and_invalid(uor, dev):
+    # k = 0: beta * C (raw.rs:253-277).
+    empty = torch.zeros(1, dtype=torch.float32, device=dev)
+    c = torch.tensor([1.0, 2.0, 3.0, 4.0], device=dev)
+    assert uor.raw_gemm(2, 0, 2, 1, empty, 0, 1, empty, 2, 1, 3, c, 2, 1) == 0
+    torch.cuda.synchronize()
+    assert c.cpu().tolist() == [3.0, 6.0, 9.0, 12.0]
+    # m = 0 or n = 0 writes nothing (raw.rs:279-311).
+    op = torch.ones(8, device=dev)
+    for m, n in [(0, 2), (2, 0), (0, 0)]:
+        u = torch.full((4,), 7.0, device=dev)
+        assert uor.raw_gemm(m, 4, n, 1, op, 4, 1, op, n, 1, 0, u, n, 1) == 0
+        torch.cuda.synchronize()
+        assert u.cpu().tolist() == [7.0] * 4
+    # A C view that maps two cells onto one is a silent no-op on the raw face.
+    u = torch.full((4,), 7.0, device=dev)
+    assert uor.raw_gemm(2, 4, 2, 1, op, 4, 1, op, 2, 1, 0, u, 0, 1) == 0
+    torch.cuda.synchronize()
+    assert u.cpu().tolist() == [7.0] * 4
+    # ... and a status on the view API.
+    st, _ = uor.gemm_float(op, (2, 4), (4, 1), op, (4, 2), (2, 1), u, (2, 2), (0, 1))
+    assert uor.STATUS[st] == "output_aliases_itself"
+    st, _ = uor.gemm_float(op, (2, 4), (4, 1), op, (3, 2), (2, 1), u, (2, 2), (2, 1))
+    assert uor.STATUS[st] == "nonconformant"
+    st, _ = uor.gemm_float(op, (2, 5), (5, 1), op, (5, 2), (2, 1), u, (2, 2), (2, 1))
+    assert uor.STATUS[st] == "short_buffer"
+
+
+def test_dgemm_and_slice_faces(oracle, uor, dev):
+    """raw.rs:321-364 (the f64 face), and slice::gemm_float_ex with padded
+    leading dimensions."""
+    m, k, n = 5, 9, 4
+    rsa, csa = -k, 1
+    abuf, aoff = strided(rsa, csa, m, k, lambda i, j: (i * k + j) * 0.25 - 1.0, np.float64)
+    b = np.array([i * -0.5 + 2.0 for i in range(k * n)], np.float64)
+    want = np.zeros(m * n, np.float64)
+    oracle.gemm_float(abuf, (m, k), (rsa, csa), b, (k, n), (n, 1), want, (m, n), (n, 1))
+    gc = torch.zeros(m * n, dtype=torch.float64, device=dev)
+    assert uor.raw_gemm(m, k, n, 1, torch.from_numpy(abuf).to(dev), rsa, csa,
+                        torch.from_numpy(b).to(dev), n, 1, 0, gc, n, 1, a_off=aoff) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(gc.cpu().numpy()), bits(want))
+    # slice face: lda = k + 3, ldb = n + 1, ldc = n + 2, alpha 3, beta -1.
+    for is64 in (False, True):
+        ft = np.float64 if is64 else np.float32
+        a2, b2 = gen.corpus_operands((m, k, n, "FewGrades", 9), is64)
+        A = np.zeros((m, k + 3), ft)
+        A[:, :k] = a2.reshape(m, k)
+        B = np.zeros((k, n + 1), ft)
+        B[:, :n] = b2.reshape(k, n)
+        C = np.arange(m * (n + 2), dtype=ft) * ft(0.125)
+        want = C.copy()
+        oracle.gemm_float(A.reshape(-1), (m, k), (k + 3, 1), B.reshape(-1), (k, n), (n + 1, 1), want,
+                          (m, n), (n + 2, 1), alpha=3, beta=-1)
+        gc = torch.from_numpy(C.copy()).to(dev)
+        assert uor.slice_gemm_float_ex(m, k, n, 3, torch.from_numpy(A.reshape(-1)).to(dev), k + 3,
+                                       torch.from_numpy(B.reshape(-1)).to(dev), n + 1, -1, gc,
+                                       n + 2) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(gc.cpu().numpy()), bits(want))
+
+
+@pytest.mark.parametrize("is64,m,k,n", [(False, 48, 4096, 40), (True, 24, 2048, 20)])
+def test_config4_distribution_reduced(oracle, uor, dev, is64, m, k, n):
+    """configs[3] entries (e in [-40, 40] f32 / [-300, 300] f64, 1% zeros, 1%
+    cancelling pairs) at the full depth, on a reduced m x n."""
+    a = gen.float_config4(m, k, is64, 9)
+    b = gen.float_config4(k, n, is64, 10)
+    a, b = gen.cancel_pairs(a, b, 99)
+    check(oracle, uor, dev, a.reshape(-1).copy(), b.reshape(-1).copy(), m, k, n)
+    check(oracle, uor, dev, a.reshape(-1).copy(), b.reshape(-1).copy(), m, k, n, mode="toward_zero")

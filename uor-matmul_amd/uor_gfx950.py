@@ -204,6 +204,27 @@ def gemm_float(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strid
     return st, r.as_dict()
 
 
+def slice_gemm_float_ex(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, scratch=None, stream=None):
+    import torch
+    return lib().uor_gfx950_slice_gemm_float_ex(
+        int(a.dtype == torch.float64), m, k, n, int(alpha), _ptr(a), a.numel(), lda, _ptr(b),
+        b.numel(), ldb, int(beta), _ptr(c), c.numel(), ldc, _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+
+
+def raw_gemm(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, a_off=0, b_off=0,
+             c_off=0, scratch=None, stream=None):
+    """raw::sgemm / dgemm: a, b, c are device tensors and *_off the element
+    index of element (0, 0) inside each (strides may be negative)."""
+    import torch
+    is64 = a.dtype == torch.float64
+    es = 8 if is64 else 4
+    f = lib().uor_gfx950_dgemm if is64 else lib().uor_gfx950_sgemm
+    return f(m, k, n, int(alpha), a.data_ptr() + a_off * es, rsa, csa, b.data_ptr() + b_off * es,
+             rsb, csb, int(beta), c.data_ptr() + c_off * es, rsc, csc, _ptr(scratch),
+             0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+
+
 def suggested_scratch_float(is64, m, k, n):
     return lib().uor_gfx950_suggested_scratch_float(int(is64), m, k, n)
 
