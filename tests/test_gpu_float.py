@@ -18,8 +18,24 @@ def bits(x):
     return x.view(np.uint64 if x.dtype == np.float64 else np.uint32)
 
 
+def offer_for(uor, dev, offer, is64, m, k, n):
+    """The scratch offer: none (direct route), the suggested size (CRT with
+    every modulus available) or an eighth of it (CRT with few moduli: wide
+    cases fall back to the direct loop cell by cell)."""
+    if offer == "none":
+        return None
+    want = uor.suggested_scratch_float(is64, m, k, n)
+    if want == 0:
+        return None
+    if offer == "small":
+        want //= 8
+    return torch.empty(want + 64, dtype=torch.uint8, device=dev)[64:]  # misaligned on purpose
+
+
 def check(oracle, uor, dev, a, b, m, k, n, c0=None, alpha=1, beta=0, mode="nearest",
-          a_strides=None, c_strides=None, scratch=None, expect_route=None):
+          a_strides=None, c_strides=None, scratch=None, expect_route=None, offer=None):
+    if offer is not None:
+        scratch = offer_for(uor, dev, offer, a.dtype == np.float64, m, k, n)
     ars = a_strides or (k, 1)
     crs = c_strides or (n, 1)
     c0 = np.zeros(m * n, a.dtype) if c0 is None else c0
@@ -42,19 +58,24 @@ def check(oracle, uor, dev, a, b, m, k, n, c0=None, alpha=1, beta=0, mode="neare
     return route
 
 
+OFFERS = ["none", "full", "small"]
+
+
+@pytest.mark.parametrize("offer", OFFERS)
 @pytest.mark.parametrize("is64", [False, True])
 @pytest.mark.parametrize("case", gen.CORRECTNESS_CASES + gen.PERFORMANCE_CASES,
                          ids=lambda c: f"{c[3]}-{c[4]}")
-def test_corpus(oracle, uor, dev, is64, case):
+def test_corpus(oracle, uor, dev, is64, case, offer):
     m, k, n = case[:3]
     a, b = gen.corpus_operands(case, is64)
     modes = MODES if m * k * n <= 4096 else ["nearest", "toward_zero"]
     for mode in modes:
-        check(oracle, uor, dev, a, b, m, k, n, mode=mode)
+        check(oracle, uor, dev, a, b, m, k, n, mode=mode, offer=offer)
 
 
+@pytest.mark.parametrize("offer", OFFERS)
 @pytest.mark.parametrize("is64", [False, True])
-def test_alpha_beta(oracle, uor, dev, is64):
+def test_alpha_beta(oracle, uor, dev, is64, offer):
     ft = np.float64 if is64 else np.float32
     rng = np.random.default_rng(11 + is64)
     m, k, n = 9, 40, 11
@@ -64,11 +85,13 @@ def test_alpha_beta(oracle, uor, dev, is64):
     for alpha, beta in [(1, 1), (3, -1), (0, 2), (-7, 0), (1 << 40, -(1 << 50)), (0, 0),
                         (-(1 << 63), 1), ((1 << 63) - 1, -(1 << 63))]:
         for mode in ("nearest", "toward_zero"):
-            check(oracle, uor, dev, a, b, m, k, n, c0=c0, alpha=alpha, beta=beta, mode=mode)
+            check(oracle, uor, dev, a, b, m, k, n, c0=c0, alpha=alpha, beta=beta, mode=mode,
+                  offer=offer)
 
 
+@pytest.mark.parametrize("offer", OFFERS)
 @pytest.mark.parametrize("is64", [False, True])
-def test_nonfinite_rows_and_columns(oracle, uor, dev, is64):
+def test_nonfinite_rows_and_columns(oracle, uor, dev, is64, offer):
     ft = np.float64 if is64 else np.float32
     m, k, n = 6, 50, 7
     a, b = gen.corpus_operands((m, k, n, "FullFiniteRange", 5), is64)
@@ -80,10 +103,20 @@ def test_nonfinite_rows_and_columns(oracle, uor, dev, is64):
     b[10 * n + 5] = np.nan         # column 5 is NaN everywhere
     a[4 * k + 7] = np.inf
     a[4 * k + 8] = -np.inf         # row 4: +inf and -inf -> NaN
+    # Narrow the finite entries so that the CRT route keeps these lines.
+    a2, b2 = gen.corpus_operands((m, k, n, "FewGrades", 6), is64)
+    fin_a, fin_b = np.isfinite(a), np.isfinite(b)
+    keep_a = np.zeros(a.shape, bool)
+    keep_a[[1 * k + 3, 2 * k + 4, 4 * k + 7, 4 * k + 8]] = True
+    keep_b = np.zeros(b.shape, bool)
+    keep_b[[3 * n + 2, 10 * n + 5]] = True
+    a = np.where(keep_a, a, a2)
+    b = np.where(keep_b, b, b2)
+    assert not fin_a.all() and not fin_b.all()
     for mode in MODES:
-        check(oracle, uor, dev, a, b, m, k, n, mode=mode)
-    check(oracle, uor, dev, a, b, m, k, n, alpha=0)
-    check(oracle, uor, dev, a, b, m, k, n, alpha=-2, beta=1, c0=np.full(m * n, ft(1.5)))
+        check(oracle, uor, dev, a, b, m, k, n, mode=mode, offer=offer)
+    check(oracle, uor, dev, a, b, m, k, n, alpha=0, offer=offer)
+    check(oracle, uor, dev, a, b, m, k, n, alpha=-2, beta=1, c0=np.full(m * n, ft(1.5)), offer=offer)
 
 
 def strided(rs, cs, rows, cols, f, ft):
@@ -187,12 +220,70 @@ def test_dgemm_and_slice_faces(oracle, uor, dev):
         assert np.array_equal(bits(gc.cpu().numpy()), bits(want))
 
 
+@pytest.mark.parametrize("offer", OFFERS)
 @pytest.mark.parametrize("is64,m,k,n", [(False, 48, 4096, 40), (True, 24, 2048, 20)])
-def test_config4_distribution_reduced(oracle, uor, dev, is64, m, k, n):
+def test_config4_distribution_reduced(oracle, uor, dev, is64, m, k, n, offer):
     """configs[3] entries (e in [-40, 40] f32 / [-300, 300] f64, 1% zeros, 1%
     cancelling pairs) at the full depth, on a reduced m x n."""
     a = gen.float_config4(m, k, is64, 9)
     b = gen.float_config4(k, n, is64, 10)
     a, b = gen.cancel_pairs(a, b, 99)
-    check(oracle, uor, dev, a.reshape(-1).copy(), b.reshape(-1).copy(), m, k, n)
-    check(oracle, uor, dev, a.reshape(-1).copy(), b.reshape(-1).copy(), m, k, n, mode="toward_zero")
+    route = check(oracle, uor, dev, a.reshape(-1).copy(), b.reshape(-1).copy(), m, k, n,
+                  offer=offer)
+    if offer == "full":
+        assert route["kind"] == "float_crt", route
+    check(oracle, uor, dev, a.reshape(-1).copy(), b.reshape(-1).copy(), m, k, n, mode="toward_zero",
+          offer=offer)
+
+
+@pytest.mark.parametrize("is64", [False, True])
+def test_crt_narrow_and_strided(oracle, uor, dev, is64):
+    """Moderate exponent spreads (every line within the CRT route), odd
+    shapes, a transposed A and column-major B and C, alpha and beta."""
+    ft = np.float64 if is64 else np.float32
+    rng = np.random.default_rng(5 + is64)
+    for m, k, n in [(1, 1, 1), (3, 70, 5), (130, 200, 129), (257, 64, 33), (64, 1000, 300)]:
+        a = (rng.standard_normal(m * k) * 2.0 ** rng.integers(-20, 20, m * k)).astype(ft)
+        b = (rng.standard_normal(k * n) * 2.0 ** rng.integers(-20, 20, k * n)).astype(ft)
+        c0 = rng.standard_normal(m * n).astype(ft)
+        sc = offer_for(uor, dev, "full", is64, m, k, n)
+        want = c0.copy()
+        oracle.gemm_float(a, (m, k), (1, m), b, (k, n), (1, k), want, (m, n), (1, m), alpha=-3,
+                          beta=2)
+        gc = torch.from_numpy(c0.copy()).to(dev)
+        st, route = uor.gemm_float(torch.from_numpy(a).to(dev), (m, k), (1, m),
+                                   torch.from_numpy(b).to(dev), (k, n), (1, k), gc, (m, n), (1, m),
+                                   alpha=-3, beta=2, scratch=sc)
+        torch.cuda.synchronize()
+        assert st == 0 and route["kind"] == "float_crt", route
+        assert np.array_equal(bits(gc.cpu().numpy()), bits(want)), (m, k, n)
+
+
+def plan_of(scratch):
+    """The CRT plan the device wrote at the start of the (256-aligned) offer:
+    (moduli used, direct fallback for every cell, bound bits)."""
+    off = (-scratch.data_ptr()) % 256
+    return scratch[off:off + 12].cpu().view(torch.int32).tolist()
+
+
+def test_crt_plan_is_tight(oracle, uor, dev):
+    """configs[3] f32 rows (e in [-40, 40]) at the full depth use the residue
+    route with the fewest moduli that cover the bound, and no fallback."""
+    m, k, n = 64, 4096, 64
+    a = gen.float_config4(m, k, False, 9)
+    b = gen.float_config4(k, n, False, 10)
+    sc = offer_for(uor, dev, "full", False, m, k, n)
+    c = torch.zeros(m * n, dtype=torch.float32, device=dev)
+    st, route = uor.gemm_float(torch.from_numpy(a.reshape(-1).copy()).to(dev), (m, k), (k, 1),
+                               torch.from_numpy(b.reshape(-1).copy()).to(dev), (k, n), (n, 1), c,
+                               (m, n), (n, 1), scratch=sc)
+    torch.cuda.synchronize()
+    nmod, off, need = plan_of(sc)
+    assert st == 0 and off == 0, (nmod, off, need)
+    # widths of about 104 bits per line and an L1 bound a few bits above the
+    # top element: well under the 4096-term worst case of 104 + 104 + 12.
+    assert 200 <= need <= 222 and 27 <= nmod <= 30, (nmod, need)
+    want = np.zeros(m * n, np.float32)
+    oracle.gemm_float(a.reshape(-1).copy(), (m, k), (k, 1), b.reshape(-1).copy(), (k, n), (n, 1),
+                      want, (m, n), (n, 1))
+    assert np.array_equal(bits(c.cpu().numpy()), bits(want))

@@ -38,6 +38,8 @@ def _compile(src: pathlib.Path) -> pathlib.Path:
 
 def main() -> pathlib.Path:
     OBJ.mkdir(exist_ok=True)
+    # The residue-number-system constants of the exact float route.
+    subprocess.run([sys.executable, str(CSRC / "gen_crt_tables.py")], check=True)
     srcs = sorted(CSRC.glob("*.hip"))
     workers = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=max(1, workers)) as ex:

@@ -27,8 +27,32 @@
 // register (carry-save; a digit slot absorbs 2^31 products before it could
 // overflow), then normalises, scales, adds beta * C and encodes.  It is the
 // exact fallback, not the fast route.
+//
+// FLOAT_CRT (when the scratch offer holds its planes and k <= 2^17) runs the
+// products on int8 MFMA through a residue number system:
+//  1. line statistics: for every row of A and column of B, the exponent of
+//     its lowest set bit (lo), its width in bits (top - lo), an upper bound
+//     of log2 of its L1 norm at that scale, and whether it holds a
+//     non-finite code.  Row i of A is then the integer vector
+//     alpha_ip = +-m_ip * 2^(x_ip - lo_i) of at most `width` bits;
+//  2. a plan kernel picks, on the device, the fewest moduli whose product M
+//     bounds every reconstructed sum X_ij = sum_p alpha_ip * beta_pj with
+//     |X| < M / 2 (|X| <= ||alpha_i||_1 * max|beta_j| and symmetrically);
+//  3. residue planes: balanced int8 residues of alpha and beta per modulus;
+//  4. one batched int8 MFMA GEMM (grid z = modulus) on the direct-to-LDS
+//     pipeline; its epilogue reduces each exact i32 sum mod p to a byte;
+//  5. the finish kernel reconstructs X_ij by the CRT with a rounded quotient
+//     (exact: |X| stays 2^-21 M away from M / 2), places X * 2^(lo_i + lo_j)
+//     into the same digit register as the direct route, and runs the same
+//     alpha / beta / encode epilogue.  Rows or columns wider than WIDE_BITS
+//     and non-finite lines take the direct loop inside this kernel, cell by
+//     cell, so every input is exact on either route and the bytes never
+//     depend on the offer.
 
-#include "common.hpp"
+#include <algorithm>
+
+#include "mfma_dl.hpp"
+#include "crt_tables.hpp"
 
 namespace uor {
 
@@ -423,25 +447,685 @@ static hipError_t launch_direct(const FArgs &F, hipStream_t s) {
     return hipGetLastError();
 }
 
+
+// --------------------------------------------------------- CRT route --
+
+constexpr int WIDE_BITS = 160;  // wider lines take the direct loop
+constexpr int CRT_BK_MAX = 1 << 17;  // i32 MFMA sums stay exact: 2^14 * k < 2^31
+
+enum : int32_t { LS_DIRTY = 1, LS_WIDE = 2, LS_EMPTY = 4 };
+
+struct LineStat {
+    int32_t lo;     // exponent of the lowest set bit over the line's finite nonzeros
+    int32_t width;  // top - lo (bits of the largest aligned integer)
+    float l1;       // upper bound of log2(sum |aligned integers|); -1e30 when empty
+    int32_t flags;
+};
+
+struct CrtHdr {
+    int32_t nmod;     // moduli in use (0: no residue work)
+    int32_t crt_off;  // 1: every cell takes the direct loop
+    int32_t need;     // the bound B used: |X| < 2^B
+    int32_t pad[61];
+};
+
+// The trimmed significand and exponent of a finite nonzero: m odd.
+__device__ inline void trim(const Dec &d, uint64_t *m, int *x) {
+    const int tz = __builtin_ctzll(d.mant);
+    *m = d.mant >> tz;
+    *x = d.exp + tz;
+}
+
+__device__ inline int bitlen64(uint64_t v) { return 64 - __builtin_clzll(v); }
+
+// Statistics of `lines` lines of `len` elements: element e of line t at
+// base + t * s_line + e * s_elem.  CONTIG (s_elem == 1): one workgroup per
+// line, threads along it; otherwise 16 lines per workgroup, 16 consecutive
+// threads across them (coalesced when s_line == 1) and 16 lanes along each.
+template <bool F64, bool CONTIG>
+__global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64_t s_line,
+                                                         int64_t s_elem, uint64_t lines,
+                                                         uint64_t len, LineStat *out) {
+    constexpr int LPB = CONTIG ? 1 : 16;  // lines per block
+    constexpr int TPL = 256 / LPB;        // threads per line
+    __shared__ int s_lo[256], s_hi[256], s_fl[256];
+    __shared__ double s_sum[256];
+    const int t = threadIdx.x;
+    const int tl = CONTIG ? 0 : (t & 15), te = CONTIG ? t : (t >> 4);
+    const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
+    const bool live = line < lines;
+    int lo = 1 << 30, hi = -(1 << 30), fl = 0;
+    if (live) {
+        for (uint64_t e = te; e < len; e += TPL) {
+            const Dec d = decode<F64>(load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
+            if (d.cls != CLS_FINITE) {
+                fl |= LS_DIRTY;
+                continue;
+            }
+            if (!d.mant) continue;
+            uint64_t m;
+            int x;
+            trim(d, &m, &x);
+            lo = min(lo, x);
+            hi = max(hi, x + bitlen64(m));
+        }
+    }
+    s_lo[t] = lo;
+    s_hi[t] = hi;
+    s_fl[t] = fl;
+    __syncthreads();
+    for (int w = TPL / 2; w >= 1; w >>= 1) {
+        if (te < w) {
+            const int o = CONTIG ? t + w : t + 16 * w;
+            s_lo[t] = min(s_lo[t], s_lo[o]);
+            s_hi[t] = max(s_hi[t], s_hi[o]);
+            s_fl[t] |= s_fl[o];
+        }
+        __syncthreads();
+    }
+    lo = s_lo[tl];
+    hi = s_hi[tl];
+    fl = s_fl[tl];
+    // Pass 2: sum of |aligned integers| scaled by 2^-(top), each term <= 1.
+    double sum = 0;
+    if (live && hi > lo) {
+        for (uint64_t e = te; e < len; e += TPL) {
+            const Dec d = decode<F64>(load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
+            if (d.cls != CLS_FINITE || !d.mant) continue;
+            uint64_t m;
+            int x;
+            trim(d, &m, &x);
+            sum += ldexp((double)m, x - hi);
+        }
+    }
+    __syncthreads();
+    s_sum[t] = sum;
+    __syncthreads();
+    for (int w = TPL / 2; w >= 1; w >>= 1) {
+        if (te < w) s_sum[t] += s_sum[CONTIG ? t + w : t + 16 * w];
+        __syncthreads();
+    }
+    if (te == 0 && live) {
+        LineStat st;
+        if (hi <= lo) {
+            st.lo = 0;
+            st.width = 0;
+            st.l1 = -1e30f;
+            st.flags = fl | LS_EMPTY;
+        } else {
+            st.lo = lo;
+            st.width = hi - lo;
+            // Rounding of the double sum is below 2^-30 relative for any
+            // reachable length; terms that underflowed are below 2^-900 each.
+            const double s = s_sum[tl] * (1.0 + 0x1p-28) + (double)len * 0x1p-900;
+            st.l1 = (float)(log2(s) + (double)(hi - lo) + 1e-6);
+            st.flags = fl | (st.width > WIDE_BITS ? LS_WIDE : 0);
+        }
+        out[line] = st;
+    }
+}
+
+// The plan: the bound B (|X_ij| < 2^B for every CRT cell) and the fewest
+// moduli whose capacity covers it; crt_off when the offer holds fewer planes.
+__global__ void __launch_bounds__(256) crt_plan_kernel(const LineStat *ra, uint64_t m,
+                                                       const LineStat *cb, uint64_t n, uint64_t k,
+                                                       int nm_alloc, CrtHdr *h) {
+    __shared__ float s_w[4][256];
+    const int t = threadIdx.x;
+    float wa = -1e30f, la = -1e30f, wb = -1e30f, lb = -1e30f;
+    for (uint64_t i = t; i < m; i += 256) {
+        const LineStat s = ra[i];
+        if (s.flags & (LS_WIDE | LS_EMPTY)) continue;
+        wa = fmaxf(wa, (float)s.width);
+        la = fmaxf(la, s.l1);
+    }
+    for (uint64_t j = t; j < n; j += 256) {
+        const LineStat s = cb[j];
+        if (s.flags & (LS_WIDE | LS_EMPTY)) continue;
+        wb = fmaxf(wb, (float)s.width);
+        lb = fmaxf(lb, s.l1);
+    }
+    s_w[0][t] = wa;
+    s_w[1][t] = la;
+    s_w[2][t] = wb;
+    s_w[3][t] = lb;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if (t < w)
+            for (int q = 0; q < 4; ++q) s_w[q][t] = fmaxf(s_w[q][t], s_w[q][t + w]);
+        __syncthreads();
+    }
+    if (t != 0) return;
+    wa = s_w[0][0];
+    la = s_w[1][0];
+    wb = s_w[2][0];
+    lb = s_w[3][0];
+    CrtHdr r{};
+    if (wa < 0 || wb < 0) {  // no CRT cell has a nonzero product
+        r.nmod = 0;
+        r.need = 0;
+    } else {
+        int lk = 0;
+        while ((1ull << lk) < k) ++lk;
+        const double b = fmin(fmin((double)la + wb, (double)wa + lb), (double)wa + wb + lk);
+        const int need = (int)ceil(b + 1e-5);
+        int nm = 0;
+        while (nm < CRT_NMAX && crt_cap[nm] < need) ++nm;
+        r.need = need;
+        if (crt_cap[nm] < need || nm > nm_alloc) r.crt_off = 1;
+        else r.nmod = nm;
+    }
+    *h = r;
+}
+
+// Balanced int8 residue of +-m * 2^s modulo crt_mod[l] (s < 256).  For
+// m < 2^45 the product m * (2^s mod p) < 2^53 is exact in a double and one
+// reduction suffices (the quotient's rounding error is below one); a wider m
+// (f64 significands) is first reduced alone.  An f32 significand (< 2^24)
+// keeps the product below 2^32.
+template <bool F64>
+__device__ inline int residue(uint64_t m, int s, bool neg, int l, const uint8_t *pow2) {
+    const int p = crt_mod[l];
+    const uint32_t w = pow2[l * 256 + s];
+    int r;
+    if (l == 0) {
+        r = (int)(((uint32_t)m * w) & 255);
+    } else if constexpr (!F64) {
+        const uint32_t x = (uint32_t)m * w;
+        const uint32_t q = (uint32_t)floor((double)x * crt_invp[l]);
+        r = (int)(x - q * (uint32_t)p);  // in [-p, 2p) as a 32-bit difference
+        if (r < 0) r += p;
+        if (r >= p) r -= p;
+    } else {
+        const double ip = crt_invp[l];
+        if (m >> 45) {
+            const double q0 = floor((double)m * ip);
+            int64_t r0 = (int64_t)m - (int64_t)q0 * p;
+            if (r0 < 0) r0 += p;
+            if (r0 >= p) r0 -= p;
+            m = (uint64_t)r0;
+        }
+        const int64_t x = (int64_t)(m * (uint64_t)w);
+        const double q = floor((double)x * ip);
+        int64_t rr = x - (int64_t)q * p;
+        if (rr < 0) rr += p;
+        if (rr >= p) rr -= p;
+        r = (int)rr;
+    }
+    int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
+    if (neg) b = -b;
+    if (b == 128) b = -128;  // p = 256: 128 and -128 are one residue
+    return b;
+}
+
+// Residue planes: plane l holds prows x ldp bytes; element (r, c) of the
+// source (r < rows, c < cols) at src + r * s_r + c * s_c, its line statistics
+// at st[STAT_ROW ? r : c].  Each thread writes 4 consecutive bytes of a plane
+// row per step of a grid-stride loop; padding (r >= rows or c >= cols) is zero.
+template <bool F64, bool STAT_ROW>
+__global__ void __launch_bounds__(256) residue_kernel(const char *src, int64_t s_r, int64_t s_c,
+                                                      uint64_t rows, uint64_t cols, uint64_t prows,
+                                                      uint64_t ldp, const LineStat *st,
+                                                      const CrtHdr *h, int8_t *planes,
+                                                      uint64_t plane_bytes) {
+    __shared__ uint32_t pow2w[CRT_NMAX * 64];
+    const int nmod = h->nmod;
+    const uint32_t *tab = (const uint32_t *)&crt_pow2[0][0];
+    for (int q = threadIdx.x; q < nmod * 64; q += 256) pow2w[q] = tab[q];
+    __syncthreads();
+    if (nmod == 0) return;
+    const uint8_t *pow2 = (const uint8_t *)pow2w;
+    const uint64_t chunks = ldp / 4, total = prows * chunks;
+    for (uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * 256) {
+        const uint64_t r = idx / chunks, c0 = (idx % chunks) * 4;
+        uint64_t mm[4];
+        int ss[4];
+        bool ok[4], ng[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint64_t c = c0 + e;
+            ok[e] = false;
+            ng[e] = false;
+            mm[e] = 0;
+            ss[e] = 0;
+            if (r >= rows || c >= cols) continue;
+            const LineStat ls = st[STAT_ROW ? r : c];
+            if (ls.flags & (LS_WIDE | LS_EMPTY)) continue;
+            const Dec d = decode<F64>(load_bits<F64>(src, (int64_t)r * s_r + (int64_t)c * s_c));
+            if (d.cls != CLS_FINITE || !d.mant) continue;
+            int x;
+            trim(d, &mm[e], &x);
+            ss[e] = x - ls.lo;
+            ng[e] = d.neg;
+            ok[e] = true;
+        }
+        int8_t *dst = planes + r * ldp + c0;
+        for (int l = 0; l < nmod; ++l) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int v = ok[e] ? residue<F64>(mm[e], ss[e], ng[e], l, pow2) : 0;
+                w |= (uint32_t)(uint8_t)(int8_t)v << (8 * e);
+            }
+            *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = w;
+        }
+    }
+}
+
+struct ResOut {
+    uint8_t *y;  // plane l at y + l * y_plane: m x n bytes, row-major
+    uint64_t y_plane;
+    uint64_t a_plane, b_plane;  // residue plane strides
+    const CrtHdr *h;
+};
+
+// One modulus per grid z: the exact i32 product of its residue planes,
+// reduced mod p into a byte per cell.
+template <int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN, 1)
+residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    using L = DlLayout<BM, BN>;
+    const int l = blockIdx.z;
+    if (l >= R.h->nmod) return;
+    A.base += (uint64_t)l * R.a_plane;
+    B.base += (uint64_t)l * R.b_plane;
+    __shared__ __attribute__((aligned(16))) char st0[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char st1[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char st2[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char st3[L::STAGE];
+    int tm, tn;
+    tile_of(gm, gn, &tm, &tn);
+    const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
+    const int nk = (int)(K / DL_BK);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int half = lane >> 5, l32 = lane & 31;
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+    dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, 0, nk, st0, st1, st2, st3, acc);
+    const int p = crt_mod[l];
+    const double invp = crt_invp[l];
+    uint8_t *y = R.y + (uint64_t)l * R.y_plane;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint64_t col = n0 + wn * (BN / WN) + 32 * j + l32;
+            const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
+            if (col >= B.mn) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint64_t row = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (row >= A.mn) continue;
+                const int v = acc[i][j][r];
+                int q;
+                if (l == 0) {
+                    q = v & 255;
+                } else {
+                    q = v - p * (int)floor((double)v * invp);
+                    if (q < 0) q += p;
+                    if (q >= p) q -= p;
+                }
+                y[row * B.mn + col] = (uint8_t)q;
+            }
+        }
+    }
+}
+
+// The CRT reconstruction of X_ij in ND 16-bit digits: |X| into D[] (each in
+// [0, 2^16)), returns true when X < 0.  Each slot sums at most 49 products of
+// a residue (< 2^8) and a 16-bit digit of M / p_l, below 2^30, so the sums
+// run on 24-bit multiply-adds in 32-bit lanes; the quotient round(sum c_l /
+// p_l) is exact in a double because |X| / M stays 2^-21 away from 1/2.
+template <int ND>
+__device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, int nmod,
+                             uint32_t (&D)[ND]) {
+    int32_t sl[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) sl[d] = 0;
+    // Every plane's byte first, so the loads overlap instead of each waiting.
+    int yb[CRT_NMAX];
+#pragma unroll
+    for (int l = 0; l < CRT_NMAX; ++l) yb[l] = l < nmod ? (int)y[(uint64_t)l * y_plane + cell] : 0;
+    double f = 0;
+    const uint16_t(*Ml)[CRT_ND16] = crt_Ml16[nmod - 1];
+    const uint16_t *inv = crt_inv[nmod - 1];
+#pragma unroll
+    for (int l = 0; l < CRT_NMAX; ++l) {
+        if (l < nmod) {
+            const int p = crt_mod[l];
+            const int prod = yb[l] * (int)inv[l];  // < 2^16
+            int c;
+            if (l == 0) {
+                c = prod & 255;
+            } else {
+                const int q = (int)((float)prod * crt_invpf[l]);
+                c = prod - q * p;
+                if (c < 0) c += p;
+                if (c >= p) c -= p;
+            }
+            f += (double)c * crt_invp[l];
+#pragma unroll
+            for (int d = 0; d < ND; ++d) sl[d] += c * (int32_t)Ml[l][d];
+        }
+    }
+    const int32_t q = (int32_t)floor(f + 0.5);
+    int32_t carry = 0;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+        const int32_t v = sl[d] - q * (int32_t)crt_M16[nmod][d] + carry;
+        D[d] = (uint32_t)(v & 0xffff);
+        carry = v >> 16;  // arithmetic: floor division
+    }
+    const bool neg = carry < 0;
+    if (neg) {
+        uint32_t c = 1;
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+            const uint32_t v = (~D[d] & 0xffff) + c;
+            D[d] = v & 0xffff;
+            c = v >> 16;
+        }
+    }
+    return neg;
+}
+
+// impl_encode_into_float (acc.rs:1734-1868) from a magnitude in N 16-bit
+// digits D[] whose bit 0 has exponent E, all in registers: the same rounding
+// as encode_reg, with every digit picked by comparison instead of indexing.
+template <bool F64, int N>
+__device__ inline uint64_t encode16(const uint32_t (&D)[N], int E, bool neg, int mode) {
+    using F = Fmt<F64>;
+    constexpr int MANT = F::MANT, EXPO = F::EXPO, P = MANT + 1;
+    constexpr uint64_t EXPMASK = (1ull << EXPO) - 1;
+    int top = -1;
+#pragma unroll
+    for (int t = 0; t < N; ++t)
+        if (D[t]) top = 16 * t + 31 - __builtin_clz(D[t]);
+    if (top < 0) return 0;  // an exact zero is +0
+    const int exp = E + top;
+    int lsb_exp = exp - (P - 1) < F::SUB_LSB ? F::SUB_LSB : exp - (P - 1);
+    const int lsb = lsb_exp - E;
+    uint64_t sig;
+    int round_bit = 0, sticky = 0;
+    if (lsb <= 0) {
+        // Every bit of X lies at or above the output's LSB: X < 2^P.
+        uint64_t x = 0;
+#pragma unroll
+        for (int t = 0; t < N && t < 4; ++t) x |= (uint64_t)D[t] << (16 * t);
+        sig = x << (-lsb);
+    } else {
+        const int q = lsb >> 4, r = lsb & 15;
+        uint64_t d0 = 0, d1 = 0, d2 = 0, d3 = 0, d4 = 0;
+        const int rb = lsb - 1, qb = rb >> 4;
+        const uint32_t below = (1u << (rb & 15)) - 1;
+#pragma unroll
+        for (int t = 0; t < N; ++t) {
+            const uint64_t v = D[t];
+            d0 = t == q ? v : d0;
+            d1 = t == q + 1 ? v : d1;
+            d2 = t == q + 2 ? v : d2;
+            d3 = t == q + 3 ? v : d3;
+            d4 = t == q + 4 ? v : d4;
+            if (t == qb) {
+                round_bit = (int)((v >> (rb & 15)) & 1);
+                if (v & below) sticky = 1;
+            }
+            if (t < qb && v) sticky = 1;
+        }
+        const uint64_t lo = d0 | (d1 << 16) | (d2 << 32) | (d3 << 48);
+        sig = ((lo >> r) | (r ? (d4 << (64 - r)) : 0)) & ((1ull << P) - 1);
+    }
+    const int inc = (mode == UOR_ENCODE_NEAREST) ? (round_bit && (sticky || (sig & 1))) : 0;
+    sig += (uint64_t)inc;
+    if (sig >> P) {
+        sig >>= 1;
+        lsb_exp += 1;
+    }
+    const uint64_t sbit = (uint64_t)(neg ? 1 : 0) << (MANT + EXPO);
+    if (sig == 0) return sbit;
+    if ((sig >> (P - 1)) == 1) {
+        const int biased = lsb_exp + (P - 1) + F::BIAS;
+        if (biased >= (int)EXPMASK) {
+            if (mode == UOR_ENCODE_NEAREST) return sbit | (EXPMASK << MANT);
+            return sbit | ((EXPMASK - 1) << MANT) | ((1ull << MANT) - 1);
+        }
+        return sbit | ((uint64_t)biased << MANT) | (sig & ((1ull << MANT) - 1));
+    }
+    return sbit | sig;
+}
+
+// The direct loop of one cell (any input), into the zeroed register R.
+template <bool F64>
+__device__ inline int direct_cell(const FArgs &F, const Reg &R, uint64_t i, uint64_t j) {
+    using Fm = Fmt<F64>;
+    constexpr int S = Fm::DIGITS;
+    int flags = 0;
+    const int64_t abase = (int64_t)i * F.ars, bbase = (int64_t)j * F.bcs;
+    for (uint64_t p = 0; p < F.k; ++p) {
+        const Dec a = decode<F64>(load_bits<F64>(F.a, abase + (int64_t)p * F.acs));
+        const Dec b = decode<F64>(load_bits<F64>(F.b, (int64_t)p * F.brs + bbase));
+        if (a.cls != CLS_FINITE || b.cls != CLS_FINITE) {
+            flags |= product_flags(a, b);
+            continue;
+        }
+        if (a.mant == 0 || b.mant == 0) continue;
+        uint64_t lo, hi;
+        if constexpr (F64) {
+            lo = a.mant * b.mant;
+            hi = __umul64hi(a.mant, b.mant);
+        } else {
+            lo = a.mant * b.mant;
+            hi = 0;
+        }
+        add_product<F64>(R, lo, hi, a.exp + b.exp - Fm::RB, a.neg != b.neg);
+        if ((p & ((1ull << 30) - 1)) == (1ull << 30) - 1) carry_mid<S>(R);
+    }
+    return flags;
+}
+
+// The flags of one cell: only the non-finite pairs matter.
+template <bool F64>
+__device__ inline int flags_cell(const FArgs &F, uint64_t i, uint64_t j) {
+    int flags = 0;
+    const int64_t abase = (int64_t)i * F.ars, bbase = (int64_t)j * F.bcs;
+    for (uint64_t p = 0; p < F.k; ++p) {
+        const Dec a = decode<F64>(load_bits<F64>(F.a, abase + (int64_t)p * F.acs));
+        const Dec b = decode<F64>(load_bits<F64>(F.b, (int64_t)p * F.brs + bbase));
+        if (a.cls != CLS_FINITE || b.cls != CLS_FINITE) flags |= product_flags(a, b);
+    }
+    return flags;
+}
+
+// One CRT cell: reconstruct, then either the register epilogue (no flags,
+// |alpha| < 2^16, beta * C zero: the common case) or the digit register in
+// LDS shared with the direct route (everything else).
+template <bool F64, int ND>
+__device__ inline void crt_cell(const FArgs &F, const Reg &R, const LineStat &sa,
+                                const LineStat &sb, int flags, int nmod, const uint8_t *y,
+                                uint64_t y_plane, uint64_t i, uint64_t j) {
+    using Fm = Fmt<F64>;
+    constexpr int S = Fm::DIGITS;
+    uint32_t D[ND + 1];
+    D[ND] = 0;
+    bool neg = false;
+    if (nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY)) {
+        uint32_t X[ND];
+        neg = crt16<ND>(y, y_plane, i * F.n + j, nmod, X);
+#pragma unroll
+        for (int d = 0; d < ND; ++d) D[d] = X[d];
+    } else {
+#pragma unroll
+        for (int d = 0; d < ND; ++d) D[d] = 0;
+    }
+    const int E = sa.lo + sb.lo;
+    const int64_t ci = (int64_t)i * F.crs + (int64_t)j * F.ccs;
+    bool c_zero = true;
+    if (F.beta != 0) {
+        const Dec dc = decode<F64>(load_bits<F64>(F.c, ci));
+        c_zero = dc.cls == CLS_FINITE && dc.mant == 0;
+    }
+    const uint64_t fa = F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha;
+    if (flags == 0 && c_zero && fa != 0 && fa < 65536) {
+        if (fa != 1) {
+            uint32_t carry = 0;
+#pragma unroll
+            for (int d = 0; d <= ND; ++d) {
+                const uint32_t v = D[d] * (uint32_t)fa + carry;
+                D[d] = v & 0xffff;
+                carry = v >> 16;
+            }
+        }
+        if (F.alpha < 0) neg = !neg;
+        store_bits<F64>(F.c, ci, encode16<F64, ND + 1>(D, E, neg, F.mode));
+        return;
+    }
+    // General case: X * 2^E into the digit register, then the shared epilogue.
+    for (int q = 0; q < S; ++q) R[q] = 0;
+    const int pos = E - Fm::RB;
+    const int q0 = pos >> 5, r = pos & 31;
+#pragma unroll
+    for (int d = 0; d < ND; d += 2) {
+        const uint32_t pair = D[d] | ((d + 1 < ND ? D[d + 1] : 0u) << 16);
+        if (!pair) continue;
+        const uint64_t w = (uint64_t)pair << r;
+        const int k0 = q0 + d / 2;
+        if (k0 < S) R[k0] += (int64_t)(w & M32);
+        if (k0 + 1 < S) R[k0 + 1] += (int64_t)(w >> 32);
+    }
+    normalise<S>(R);
+    finish_cell<F64>(F, R, neg, flags, i, j);
+}
+
+template <bool F64, int TM, int TN>
+__global__ void __launch_bounds__(TM * TN) crt_finish_kernel(FArgs F, const LineStat *ra,
+                                                             const LineStat *cb, const CrtHdr *h,
+                                                             const uint8_t *y, uint64_t y_plane,
+                                                             int gn) {
+    using Fm = Fmt<F64>;
+    constexpr int S = Fm::DIGITS, NT = TM * TN;
+    __shared__ int64_t regs[S * NT];
+    const int t = threadIdx.x;
+    const uint64_t i = (uint64_t)(blockIdx.x / gn) * TM + t / TN;
+    const uint64_t j = (uint64_t)(blockIdx.x % gn) * TN + t % TN;
+    if (i >= F.m || j >= F.n) return;
+    const Reg R{regs + t, NT};
+    const CrtHdr hd = *h;
+    const LineStat sa = ra[i], sb = cb[j];
+    if (hd.crt_off || ((sa.flags | sb.flags) & LS_WIDE)) {
+        for (int q = 0; q < S; ++q) R[q] = 0;
+        const int flags = direct_cell<F64>(F, R, i, j);
+        const bool neg = normalise<S>(R);
+        finish_cell<F64>(F, R, neg, flags, i, j);
+        return;
+    }
+    const int flags = ((sa.flags | sb.flags) & LS_DIRTY) ? flags_cell<F64>(F, i, j) : 0;
+    const int nd = crt_nd16[hd.nmod];
+    if (nd <= 8) crt_cell<F64, 8>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
+    else if (nd <= 12) crt_cell<F64, 12>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
+    else if (nd <= 16) crt_cell<F64, 16>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
+    else crt_cell<F64, CRT_ND16>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
+}
+
+// Scratch layout of the CRT route for nm planes (every piece 256-aligned).
+struct CrtLayout {
+    uint64_t hdr, ra, cb, ap, bp, y, total;
+    uint64_t kp, np, a_plane, b_plane, y_plane;
+};
+
+static inline uint64_t al256(uint64_t v) { return (v + 255) & ~255ull; }
+
+static CrtLayout crt_layout(uint64_t m, uint64_t k, uint64_t n, int nm) {
+    CrtLayout L;
+    L.kp = (k + DL_BK - 1) / DL_BK * DL_BK;
+    L.np = (n + 15) / 16 * 16;
+    L.a_plane = al256(m * L.kp);
+    L.b_plane = al256(L.kp * L.np);
+    L.y_plane = al256(m * n);
+    L.hdr = 0;
+    L.ra = 256;
+    L.cb = L.ra + al256(m * sizeof(LineStat));
+    L.ap = L.cb + al256(n * sizeof(LineStat));
+    L.bp = L.ap + (uint64_t)nm * L.a_plane;
+    L.y = L.bp + (uint64_t)nm * L.b_plane;
+    L.total = L.y + (uint64_t)nm * L.y_plane;
+    return L;
+}
+
+template <bool F64>
+static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, int nm,
+                             hipStream_t s) {
+    const uint64_t m = F.m, k = F.k, n = F.n;
+    CrtHdr *h = (CrtHdr *)(scratch + L.hdr);
+    LineStat *ra = (LineStat *)(scratch + L.ra), *cb = (LineStat *)(scratch + L.cb);
+    int8_t *ap = (int8_t *)(scratch + L.ap), *bp = (int8_t *)(scratch + L.bp);
+    uint8_t *y = (uint8_t *)(scratch + L.y);
+    // 1. line statistics: rows of A (elements along acs), columns of B (along brs).
+    if (F.acs == 1)
+        hipLaunchKernelGGL((line_stats_kernel<F64, true>), dim3((unsigned)m), dim3(256), 0, s, F.a, F.ars,
+                           F.acs, m, k, ra);
+    else
+        hipLaunchKernelGGL((line_stats_kernel<F64, false>), dim3((unsigned)((m + 15) / 16)), dim3(256), 0,
+                           s, F.a, F.ars, F.acs, m, k, ra);
+    if (F.brs == 1)
+        hipLaunchKernelGGL((line_stats_kernel<F64, true>), dim3((unsigned)n), dim3(256), 0, s, F.b, F.bcs,
+                           F.brs, n, k, cb);
+    else
+        hipLaunchKernelGGL((line_stats_kernel<F64, false>), dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
+                           s, F.b, F.bcs, F.brs, n, k, cb);
+    // 2. plan.
+    hipLaunchKernelGGL(crt_plan_kernel, dim3(1), dim3(256), 0, s, ra, m, cb, n, k, nm, h);
+    // 3. residue planes: A as [m][kp], B as [kp][np].
+    {
+        const uint64_t ta = m * (L.kp / 4), tb = L.kp * (L.np / 4);
+        const auto blocks = [](uint64_t t) { return (unsigned)std::min<uint64_t>((t + 255) / 256, 2048); };
+        hipLaunchKernelGGL((residue_kernel<F64, true>), dim3(blocks(ta)), dim3(256), 0, s, F.a, F.ars,
+                           F.acs, m, k, m, L.kp, ra, h, ap, L.a_plane);
+        hipLaunchKernelGGL((residue_kernel<F64, false>), dim3(blocks(tb)), dim3(256), 0, s, F.b, F.brs,
+                           F.bcs, k, n, L.kp, L.np, cb, h, bp, L.b_plane);
+    }
+    // 4. residue GEMMs, one grid z per modulus.
+    {
+        constexpr int BM = 256, BN = 256;
+        Opnd A{ap, (int64_t)L.kp, 1, m};
+        Opnd B{bp, 1, (int64_t)L.np, n};
+        ResOut R{y, L.y_plane, L.a_plane, L.b_plane, h};
+        const int gm = (int)((m + BM - 1) / BM), gn = (int)((n + BN - 1) / BN);
+        hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4>), dim3((unsigned)(gm * gn), 1, (unsigned)nm),
+                           dim3(512), 0, s, A, B, L.kp, gm, gn, R);
+    }
+    // 5. reconstruction, epilogue, encode.
+    {
+        constexpr int TM = F64 ? 1 : 4, TN = 64;
+        const uint64_t gm = (m + TM - 1) / TM, gn = (n + TN - 1) / TN;
+        hipLaunchKernelGGL((crt_finish_kernel<F64, TM, TN>), dim3((unsigned)(gm * gn)), dim3(TM * TN), 0, s,
+                           F, ra, cb, h, y, L.y_plane, (int)gn);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace uor
 
 using namespace uor;
 
 extern "C" uint64_t uor_gfx950_suggested_scratch_float(int is_f64, uint64_t m, uint64_t k,
                                                        uint64_t n) {
+    // The CRT route's planes for every modulus it may use, plus alignment
+    // slack; 0 where that route does not apply (the direct route needs none).
     (void)is_f64;
-    (void)m;
-    (void)k;
-    (void)n;
-    return 0;
+    if (m == 0 || n == 0 || k == 0 || k > (uint64_t)CRT_BK_MAX) return 0;
+    return crt_layout(m, k, n, CRT_NMAX).total + 256;
 }
 
 extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_view *b,
                                      const uor_view *c, int64_t alpha, int64_t beta, int encode,
                                      void *scratch, uint64_t scratch_bytes, void *stream,
                                      uor_route *route) {
-    (void)scratch;
-    (void)scratch_bytes;
     route_set(route, UOR_ROUTE_NONE);
     if (!valid_encode(encode)) return UOR_INVALID_ARGUMENT;
     const int elem = is_f64 ? 8 : 4;
@@ -454,6 +1138,38 @@ extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_vi
     FArgs F{A.base, A.rs, A.cs, B.base, B.rs, B.cs, C.base, C.rs, C.cs,
             A.rows, A.cols, B.cols, alpha, beta, encode};
     hipStream_t s = (hipStream_t)stream;
+    // The CRT route when the offer holds at least one modulus' planes.
+    int nm = 0;
+    CrtLayout L{};
+    char *sc = nullptr;
+    if (scratch && F.k > 0 && F.k <= (uint64_t)CRT_BK_MAX) {
+        const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+        const uint64_t have = scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
+        sc = (char *)p1;
+        for (int q = CRT_NMAX; q >= 1; --q) {
+            const CrtLayout Lq = crt_layout(F.m, F.k, F.n, q);
+            if (Lq.total <= have) {
+                nm = q;
+                L = Lq;
+                break;
+            }
+        }
+        const uint64_t gm = (F.m + 255) / 256, gn = (F.n + 255) / 256;
+        if (gm * gn > 0x7fffffffull || F.m > 0x7fffffffull || F.n > 0x7fffffffull) nm = 0;
+    }
+    if (nm > 0) {
+        UOR_HIP(is_f64 ? launch_crt<true>(F, sc, L, nm, s) : launch_crt<false>(F, sc, L, nm, s));
+        if (route) {
+            route->kind = UOR_ROUTE_FLOAT_CRT;
+            route->tile_m = route->tile_n = 256;
+            route->tile_k = DL_BK;
+            route->split_k = 1;
+            route->launches = 7;
+            route->moduli = nm;  // planes offered; the device uses the fewest that suffice
+            route->scratch_used = L.total;
+        }
+        return UOR_OK;
+    }
     UOR_HIP(is_f64 ? launch_direct<true>(F, s) : launch_direct<false>(F, s));
     if (route) {
         route->kind = A.cols == 0 ? UOR_ROUTE_EPILOGUE_ONLY : UOR_ROUTE_FLOAT_DIRECT;

@@ -27,12 +27,9 @@
 
 #include <type_traits>
 
-#include "common.hpp"
+#include "mfma_dl.hpp"
 
 namespace uor {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int KCHUNK = 65536;
 constexpr int NTHREADS = 256;
@@ -45,14 +42,6 @@ enum : int {
 };
 
 enum : int { EPI_FUSED = 0, EPI_PARTIAL = 1, EPI_WIDE = 2 };
-
-// A placed operand seen from the reduction: element (mn, p) is at
-// base + mn*s_mn + p*s_k.
-struct Opnd {
-    const int8_t *base;
-    int64_t s_mn, s_k;
-    uint64_t mn;  // extent along m (A) or n (B)
-};
 
 struct OutArgs {
     char *base;  // element (0,0) of C
@@ -284,24 +273,6 @@ __device__ inline void partial_block(const OutArgs &o, const int *park, uint64_t
     }
 }
 
-// Tile index -> (tile row, tile column).  Workgroups are dealt round-robin to
-// the 8 XCDs, so consecutive ids are remapped onto one XCD first, then walked
-// in groups of 8 tile rows so that the tiles one XCD holds at a time share
-// A rows and B columns in its L2.
-__device__ inline void tile_of(int gm, int gn, int *tm, int *tn) {
-    int nb = gm * gn;
-    int b = blockIdx.x;
-    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
-    const int G = 8;
-    int per = G * gn;
-    int g = b / per;
-    int first = g * G;
-    int gs = min(gm - first, G);
-    int w = b - g * per;
-    *tm = first + w % gs;
-    *tn = w / gs;
-}
-
 // ------------------------------------------------------------------ kernel --
 
 template <int BM, int BN, int BK, int MA, int MB, int EPI, bool FAST>
@@ -448,163 +419,13 @@ gemm_i8_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm,
     }
 }
 
-// ------------------------------------------------- direct-to-LDS pipeline --
-//
-// The row-major x row-major case (A's reduction axis contiguous, B's n axis
-// contiguous) with k a multiple of 64 and n of 16 streams both operands
-// straight from global memory into LDS (global_load_lds_dwordx4: lane L of an
-// instruction lands at base + 16*L), NSTAGE stages deep, so each wave keeps
-// three k-steps of loads in flight while its MFMAs run.  B stays row-major
-// ([k][n]) in LDS and reaches the MFMA through ds_read_b64_tr_b8, which
-// transposes 8x8 bytes across each 16-lane group: output lane t, byte b is
-// byte t%8 of the row addressed by lane 2b + t/8.
-//
-// LDS swizzles (16-byte granularity) keep every read pass on distinct banks:
-//   A stage: row r, k-chunk c at r*64 + 16*(c ^ ((r >> 2) & 3))
-//   B stage: k-row k, n-chunk x at k*BN + 16*(x ^ (2*(k & 7) & (BN/16 - 1)))
-
-typedef int v2i __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) v2i lds_v2i;
-typedef __attribute__((address_space(3))) void lds_void;
-
-#ifndef UOR_DL_ASM
-#define UOR_DL_ASM 1
-#endif
-
-constexpr int DL_BK = 64;
-constexpr int DL_NSTAGE = 4;
-
-template <int BM, int BN>
-struct DlLayout {
-    static constexpr int A_BYTES = BM * DL_BK;
-    static constexpr int B_BYTES = BN * DL_BK;
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int BYTES = DL_NSTAGE * STAGE;
-    __device__ static inline int a_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
-    __device__ static inline int b_swz(int k) { return (2 * (k & 7)) & (BN / 16 - 1); }
-    __device__ static inline int b_off(int k, int x) { return k * BN + 16 * (x ^ b_swz(k)); }
-};
-
-template <int N>
-__device__ inline void wait_vm() {
-    // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt split in [3:0] and [15:14]),
-    // leaving expcnt and lgkmcnt unconstrained.
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// A workgroup barrier without the release fence __syncthreads() carries: the
-// fence would wait for every LDS-DMA load in flight (all stages), while each
-// thread has already waited (vmcnt) for the one stage the next step reads.
-// The empty asm statements keep the compiler from moving LDS accesses across.
-__device__ inline void stage_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// One 16-byte-per-lane global -> LDS load: lane L's 16 bytes land at
-// lds + 16*L.  Issued through inline assembly so the compiler's wait
-// insertion, which cannot tell the four stages apart across the loop's back
-// edge, does not drain every stage before a read; the explicit vmcnt waits in
-// the k loop order each stage instead.
-// M0 is reserved by the compiler, which warns on the clobber; the kernels that
-// call this make no other use of M0 (checked in their ISA).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ inline void lds_dma16(const int8_t *g, char *lds) {
-#if UOR_DL_ASM
-    const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(l)), "v"(g)
-                 : "memory", "m0");
-#else
-    __builtin_amdgcn_global_load_lds((const void *)g, (lds_void *)lds, 16, 0, 0);
-#endif
-}
-#pragma clang diagnostic pop
-
-template <int BM, int BN, int NT>
-__device__ inline void dl_issue(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t k0,
-                                char *stage) {
-    using L = DlLayout<BM, BN>;
-    constexpr int PA = BM * 4 / NT, PB = BN * 4 / NT;  // 16-byte chunks per thread
-    static_assert(PA >= 1 && PB >= 1, "tile too small for the workgroup");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // A: BM*4 chunks, slot s = row*4 + physical chunk.
-#pragma unroll
-    for (int i = 0; i < PA; ++i) {
-        const int base = (wave * PA + i) * 64;
-        const int slot = base + lane;
-        const int row = slot >> 2, pc = slot & 3;
-        const int c = pc ^ ((row >> 2) & 3);
-        uint64_t gr = m0 + row;
-        if (gr >= A.mn) gr = A.mn - 1;  // rows past m are computed and discarded
-        lds_dma16(A.base + (int64_t)gr * A.s_mn + (int64_t)(k0 + 16 * c), stage + base * 16);
-    }
-    // B: BN/16 chunks per k-row, slot s = k*(BN/16) + physical chunk.
-    char *bst = stage + L::A_BYTES;
-#pragma unroll
-    for (int i = 0; i < PB; ++i) {
-        const int base = (wave * PB + i) * 64;
-        const int slot = base + lane;
-        const int k = slot / (BN / 16), px = slot % (BN / 16);
-        const int x = px ^ L::b_swz(k);
-        uint64_t gn = n0 + 16 * x;
-        if (gn >= B.mn) gn = 0;  // columns past n are computed and discarded
-        lds_dma16(B.base + (int64_t)(k0 + k) * B.s_k + (int64_t)gn, bst + base * 16);
-    }
-}
-
-// One k-step of 64 from LDS stage `sa` (A) / `sb` (B): each wave's FM x FN
-// 32x32 blocks, two 32-deep MFMAs each.
-template <int BM, int BN, int WM, int WN>
-__device__ inline void dl_compute(const char *sa, const char *sb,
-                                  v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
-    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
-    using L = DlLayout<BM, BN>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int half = lane >> 5, l32 = lane & 31;
-    const int grp = lane >> 4, t16 = lane & 15;
-    v4i af[2][FM];
-    v4i bf[2][FN];
-#pragma unroll
-    for (int ks = 0; ks < DL_BK / 32; ++ks) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-            af[ks][i] = *(const v4i *)(sa + L::a_off(wm * (BM / WM) + 32 * i + l32, 2 * ks + half));
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int nb = wn * (BN / WN) + 32 * j + 16 * (grp & 1) + 8 * (t16 & 1);
-            const int k = 32 * ks + 16 * (grp >> 1) + (t16 >> 1);
-            v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                (lds_v2i *)(sb + L::b_off(k, nb >> 4) + (nb & 8)));
-            v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                (lds_v2i *)(sb + L::b_off(k + 8, nb >> 4) + (nb & 8)));
-            bf[ks][j] = v4i{lo[0], lo[1], hi[0], hi[1]};
-        }
-    }
-#pragma unroll
-    for (int ks = 0; ks < DL_BK / 32; ++ks)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
-}
-
 // WM x WN waves of 64 lanes (4 waves: one per SIMD, 128x128 each at BM=BN=256;
 // 8 waves: two per SIMD, so one wave's LDS reads overlap the other's MFMAs).
 template <int BM, int BN, int WM, int WN, int EPI, bool FAST, int OB>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
 gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm, int gn) {
-    constexpr int NT = 64 * WM * WN;
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     using L = DlLayout<BM, BN>;
-    constexpr int LOADS = (BM + BN) * 4 / NT;  // global_load_lds per thread per stage
-    static_assert(DL_NSTAGE == 4, "the k loop below is unrolled by four stages");
     static_assert(WM * WN * (32 * 33) * 4 <= 2 * L::STAGE, "epilogue parking fits two stages");
     // One LDS object per stage, so that every read names the stage it reads.
     __shared__ __attribute__((aligned(16))) char st0[L::STAGE];
@@ -632,32 +453,7 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
-    if (0 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg, st0);
-    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + DL_BK, st1);
-    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + 2 * DL_BK, st2);
-
-    // Step kt reads stage kt % 4 and refills stage (kt + 3) % 4, last read at
-    // step kt - 1, which every wave has finished once it passes the barrier.
-#define UOR_DL_STEP(CUR, NXT)                                                                  \
-    {                                                                                          \
-        const int ahead = min(DL_NSTAGE - 2, nk - 1 - kt);                                     \
-        if (ahead >= 2) wait_vm<2 * LOADS>();                                                  \
-        else if (ahead == 1) wait_vm<LOADS>();                                                 \
-        else wait_vm<0>();                                                                     \
-        stage_barrier();                                                                       \
-        if (kt + DL_NSTAGE - 1 < nk)                                                           \
-            dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + (uint64_t)(kt + DL_NSTAGE - 1) * DL_BK, NXT); \
-        dl_compute<BM, BN, WM, WN>(CUR, CUR + L::A_BYTES, acc);                                \
-        if (++kt >= nk) break;                                                                 \
-    }
-    for (int kt = 0; kt < nk;) {
-        UOR_DL_STEP(st0, st3)
-        UOR_DL_STEP(st1, st0)
-        UOR_DL_STEP(st2, st1)
-        UOR_DL_STEP(st3, st2)
-    }
-#undef UOR_DL_STEP
-    wait_vm<0>();
+    dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc);
     __syncthreads();
 
     if constexpr (EPI == EPI_FUSED && FAST && OB <= 4 && WM * WN == 8 && FM * FN == 8) {
