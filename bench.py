@@ -138,6 +138,50 @@ def bench_i8(args, torch, uor, gen):
     return result, (a, b, c0)
 
 
+def bench_deep(args, torch, uor):
+    """configs[1] deep case: m = n = 128, k = 2^24, A = B = all -128 (2 GiB
+    each), i64 output (every cell 2^38) with the suggested scratch offer (the
+    split-K route).  HBM-bound: 2 * 128 * 2^24 bytes per call."""
+    m = n = 128
+    k = 1 << 24
+    dev = torch.device("cuda:0")
+    a = torch.full((m * k,), -128, dtype=torch.int8, device=dev)
+    b = torch.full((k * n,), -128, dtype=torch.int8, device=dev)
+    c = torch.zeros(m * n, dtype=torch.int64, device=dev)
+    sc = torch.empty(uor.suggested_scratch_i8(m, k, n), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    route = {}
+
+    def step():
+        st, r = uor.gemm_i8(a, (m, k), (k, 1), b, (k, n), (n, 1), c, (m, n), (n, 1), out="i64",
+                            scratch=sc, stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"deep status {st}")
+        route.update(r)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    steps = max(3, min(args.steps, 10))
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(steps):
+        step()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    ms = s0.elapsed_time(s1) / steps
+    parity = bool((c == (1 << 38)).all().item())
+    nbytes = 2 * m * k + 8 * m * n
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"m": m, "n": n, "k": k, "out": "i64", "ms_per_call": round(ms, 4),
+           "GB_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+           "TOPS": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1), "route": route.get("kind"),
+           "split_k": route.get("split_k"), "parity": parity}
+    del a, b, c, sc
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
     """the 4-bit LUT decode GEMM, m in {1, 8, 32}, k = 8192,
     n = 28672, one codebook per 128 coded rows.  Three distinct code buffers
@@ -231,6 +275,75 @@ def bench_trop(args, torch, uor, gen):
             "kernel": "trop_i8_kernel", "bound": "valu"}
 
 
+def bench_float(args, torch, uor, gen):
+    """exact f32 GEMM at m = n = k = 4096 (random sign x [1, 2) x
+    2^e, e in [-40, 40], 1% zeros, 1% cancelling pairs) with the suggested
+    scratch offer (the CRT route), checked bit for bit against the direct
+    route; and the f64 variant at 2048^3 with e in [-300, 300]."""
+    dev = torch.device("cuda:0")
+    out = []
+    for is64, N in ((False, 4096), (True, 2048)):
+        a = gen.float_config4(N, N, is64, 9)
+        b = gen.float_config4(N, N, is64, 10)
+        a, b = gen.cancel_pairs(a, b, 99)
+        ga = torch.from_numpy(a.reshape(-1).copy()).to(dev)
+        gb = torch.from_numpy(b.reshape(-1).copy()).to(dev)
+        del a, b
+        c = torch.zeros(N * N, dtype=torch.float64 if is64 else torch.float32, device=dev)
+        size = uor.suggested_scratch_float(is64, N, N, N)
+        sc = torch.empty(size, dtype=torch.uint8, device=dev) if size else None
+        stream = torch.cuda.current_stream()
+        route = {}
+
+        def step(scr):
+            st, r = uor.gemm_float(ga, (N, N), (N, 1), gb, (N, N), (N, 1), c, (N, N), (N, 1),
+                                   scratch=scr, stream=stream.cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"gemm_float status {st}")
+            route.update(r)
+
+        step(sc)
+        torch.cuda.synchronize()
+        plan = None
+        if sc is not None:
+            off = (-sc.data_ptr()) % 256
+            plan = sc[off:off + 12].cpu().view(torch.int32).tolist()
+        steps = max(1, min(args.steps, 10)) if not is64 else 1
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(steps):
+            step(sc)
+        s1.record(stream)
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / steps
+        fast = c.clone()
+        kind = route.get("kind")
+        parity = None
+        if sc is not None:
+            step(None)
+            torch.cuda.synchronize()
+            parity = bool(torch.equal(fast.view(torch.int64 if is64 else torch.int32),
+                                      c.view(torch.int64 if is64 else torch.int32)))
+        run = {"format": "f64" if is64 else "f32", "m": N, "n": N, "k": N,
+               "exponents": "[-300, 300]" if is64 else "[-40, 40]", "route": kind,
+               "ms_per_call": round(ms, 4),
+               "exact_TFLOP_s": round(2.0 * N ** 3 / (ms * 1e-3) / 1e12, 2),
+               "parity_vs_direct_route": parity}
+        if plan and plan[0] == 0 and not plan[1]:
+            run["cells"] = "every line wider than the residue route's 160 bits: per-cell direct loop"
+        if plan and plan[0] and not plan[1]:
+            nmod = plan[0]
+            kp = (N + 63) // 64 * 64
+            run["moduli"] = nmod
+            run["bound_bits"] = plan[2]
+            run["int8_TOPS_issued"] = round(2.0 * N * N * kp * nmod / (ms * 1e-3) / 1e12, 1)
+            run["frac_int8_mfma_peak"] = round(run["int8_TOPS_issued"] / PEAK_INT8_TOPS, 4)
+        out.append(run)
+        del ga, gb, c, sc, fast
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline_i8(host, oracle):
     """The reference's packed route restated (oracle/fastroute.cpp) on a row
     slab of the same 8192^3 problem, all usable host cores."""
@@ -275,6 +388,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-lut", action="store_true", help="skip the secondary LUT decode figure")
     ap.add_argument("--no-trop", action="store_true", help="skip the secondary max-plus figure")
+    ap.add_argument("--no-float", action="store_true", help="skip the secondary exact-float figure")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device-to-device copy and exit (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -297,6 +411,12 @@ def main():
     import gen
     uor.lib()
     result, host = bench_i8(args, torch, uor, gen)
+    log("[bench] deep reduction")
+    result["deep"] = {
+        "metric": "deep exact i8 GEMM GB/s (% HBM peak)",
+        "config": "BASELINE configs[1] deep case: m=n=128, k=2^24, A=B=-128, i64 out",
+        "run": bench_deep(args, torch, uor),
+    }
     if not args.no_lut:
         log("[bench] lut4 decode")
         lut = bench_lut4(args, torch, uor, gen)
@@ -314,6 +434,13 @@ def main():
             "metric": "Trop<i8> max-plus terms/s (% packed-i16 VALU peak)",
             "config": "BASELINE configs[4]: m=n=k=4096, 5% -inf entries, Trop<i32> output",
             "run": bench_trop(args, torch, uor, gen),
+        }
+    if not args.no_float:
+        log("[bench] exact float")
+        result["float"] = {
+            "metric": "exact float GEMM TFLOP/s (2mnk per second, rounded once)",
+            "config": "BASELINE configs[3]",
+            "runs": bench_float(args, torch, uor, gen),
         }
     if not args.no_cpu_baseline:
         from oracle import oracle
