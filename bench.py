@@ -46,6 +46,23 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+SETTLE_S = 0.3  # untimed running before each timed region, so clocks reach steady state
+
+
+def settle(torch, step, seconds=SETTLE_S):
+    """Run `step` untimed for at least `seconds` of wall time (MI355X raises
+    its shader clock over the first ~0.2 s of sustained load; a timed region
+    that starts cold measures the ramp, not the kernel)."""
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+        n += 4
+    return n
+
+
 def load_traffic(name):
     p = ROOT / "profiles" / f"{name}.traffic.json"
     if p.exists():
@@ -77,6 +94,7 @@ def bench_i8(args, torch, uor, gen):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    settled = settle(torch, step)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     log(f"[bench] timing {args.steps} steps")
     torch.cuda.synchronize()
@@ -89,13 +107,13 @@ def bench_i8(args, torch, uor, gen):
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end) / args.steps
 
-    # Parity after timing: W+K applications of C := 3AB - C leave C0 (even)
+    # Parity after timing: W+S+K applications of C := 3AB - C leave C0 (even)
     # or 3AB - C0 (odd); compare every cell in float64 (exact below 2^53).
     log("[bench] verifying output")
     A = ga.view(N, LD)[:, :N].to(torch.float64)
     B = gb.view(N, LD)[:, :N].to(torch.float64)
     C0 = torch.from_numpy(c0).to(dev).view(N, LD)[:, :N].to(torch.float64)
-    want = C0 if (args.warmup + args.steps) % 2 == 0 else 3 * (A @ B) - C0
+    want = C0 if (args.warmup + settled + args.steps) % 2 == 0 else 3 * (A @ B) - C0
     parity = bool(torch.equal(gc.view(N, LD)[:, :N].to(torch.float64), want))
     del A, B, C0, want
 
@@ -118,6 +136,7 @@ def bench_i8(args, torch, uor, gen):
             "workload": "slice::gemm_ex i8 x i8 -> i32, m=n=k=8192, lda=ldb=ldc=8256, "
                         "alpha=3, beta=-1, C0 uniform [-2^20, 2^20] (BASELINE configs[1])",
             "m": N, "n": N, "k": N, "ld": LD, "alpha": 3, "beta": -1, "out": "i32",
+            "settle": f">= {SETTLE_S} s untimed ({settled} steps) after the warmup steps",
         },
         "parity": parity,
         "wall_s": round(wall, 4),
@@ -162,7 +181,8 @@ def bench_deep(args, torch, uor):
     for _ in range(2):
         step()
     torch.cuda.synchronize()
-    steps = max(3, min(args.steps, 10))
+    settle(torch, step)
+    steps = max(3, min(args.steps, 20))
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s0.record(stream)
     for _ in range(steps):
@@ -210,6 +230,7 @@ def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
         for i in range(args.warmup):
             step(i)
         torch.cuda.synchronize()
+        settle(torch, lambda: step(0))
         steps = max(args.steps, 30)
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s0.record(stream)
@@ -259,7 +280,8 @@ def bench_trop(args, torch, uor, gen):
     for _ in range(max(1, args.warmup)):
         step()
     torch.cuda.synchronize()
-    steps = max(args.steps, 10)
+    settle(torch, step)
+    steps = max(10, min(args.steps, 50))
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s0.record(stream)
     for _ in range(steps):
@@ -304,11 +326,13 @@ def bench_float(args, torch, uor, gen):
 
         step(sc)
         torch.cuda.synchronize()
+        if not is64:
+            settle(torch, lambda: step(sc))
         plan = None
         if sc is not None:
             off = (-sc.data_ptr()) % 256
             plan = sc[off:off + 12].cpu().view(torch.int32).tolist()
-        steps = max(1, min(args.steps, 10)) if not is64 else 1
+        steps = max(1, min(args.steps, 20)) if not is64 else 1
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s0.record(stream)
         for _ in range(steps):
@@ -383,8 +407,8 @@ def cpu_baseline_i8(host, oracle):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-lut", action="store_true", help="skip the secondary LUT decode figure")
     ap.add_argument("--no-trop", action="store_true", help="skip the secondary max-plus figure")

@@ -264,3 +264,51 @@ def test_config2_deep_k_2_24(uor, dev, out, alpha, beta, encode):
     else:
         want = [max(mn, min(mx, v)) for v in want]
     assert gc.cpu().tolist() == want
+
+
+@pytest.mark.parametrize("case", ["vec", "ldc_odd", "c_offset", "beta0", "wrap_alpha", "sat_alpha",
+                                  "i16", "i64"])
+def test_fused_tile_epilogues(uor, dev, case):
+    """The 256x256 direct-to-LDS tile (>= 256 output tiles, n a multiple of
+    16) with each epilogue branch: 16-byte i32 rows (vec), an odd ldc or a C
+    base off 16-byte alignment (per-element i32), beta = 0, alpha large
+    enough to saturate or wrap, and i16 / i64 outputs.  Expected values from
+    an exact float64 product (|sum| <= 512 * 2^14) and a numpy encode."""
+    m = n = 4096
+    k = 512
+    lda, ldb = k + 64, n + 32
+    ldc = n + (1 if case == "ldc_odd" else 4)
+    off = 1 if case == "c_offset" else 0
+    out = {"i16": "i16", "i64": "i64"}.get(case, "i32")
+    alpha, beta, encode = 3, -1, "nearest"
+    if case == "beta0":
+        beta = 0
+    if case == "wrap_alpha":
+        alpha, beta, encode = (1 << 12) + 7, 5, "wrapping"
+    if case == "sat_alpha":
+        alpha, beta, encode = (1 << 12) + 7, -5, "saturating"
+    rng = np.random.default_rng(len(case))
+    dt = {"i16": np.int16, "i32": np.int32, "i64": np.int64}[out]
+    a = torch.from_numpy(rng.integers(-128, 128, m * lda).astype(np.int8)).to(dev)
+    b = torch.from_numpy(rng.integers(-128, 128, k * ldb).astype(np.int8)).to(dev)
+    c0 = rng.integers(-(1 << 14), 1 << 14, m * ldc + off).astype(dt)
+    c = torch.from_numpy(c0.copy()).to(dev)
+    cv = c[off:]
+    st, route = uor.gemm_i8(a, (m, k), (lda, 1), b, (k, n), (ldb, 1), cv, (m, n), (ldc, 1), out=out,
+                            alpha=alpha, beta=beta, encode=encode)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == 256, route
+    S = (a.view(m, lda)[:, :k].double() @ b.view(k, ldb)[:, :n].double()).cpu().numpy().astype(np.int64)
+    C0 = c0[off:off + m * ldc].reshape(m, ldc)[:, :n].astype(np.int64)
+    x = alpha * S + beta * C0
+    bits = 8 * np.dtype(dt).itemsize
+    if encode == "wrapping":
+        want = x.astype(dt)  # two's complement truncation (numpy casts wrap)
+    else:
+        info = np.iinfo(dt)
+        want = np.clip(x, info.min, info.max).astype(dt)
+    got = c.cpu().numpy()[off:off + m * ldc].reshape(m, ldc)
+    assert np.array_equal(got[:, :n], want), case
+    # padding columns untouched
+    assert np.array_equal(got[:, n:], c0[off:off + m * ldc].reshape(m, ldc)[:, n:])
+    assert bits in (16, 32, 64)

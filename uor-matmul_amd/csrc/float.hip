@@ -722,7 +722,7 @@ struct ResOut {
 
 // One modulus per grid z: the exact i32 product of its residue planes,
 // reduced mod p into a byte per cell.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool PF>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
 residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
@@ -731,10 +731,8 @@ residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
     if (l >= R.h->nmod) return;
     A.base += (uint64_t)l * R.a_plane;
     B.base += (uint64_t)l * R.b_plane;
-    __shared__ __attribute__((aligned(16))) char st0[L::STAGE];
-    __shared__ __attribute__((aligned(16))) char st1[L::STAGE];
-    __shared__ __attribute__((aligned(16))) char st2[L::STAGE];
-    __shared__ __attribute__((aligned(16))) char st3[L::STAGE];
+    __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
+    char *st0 = lds, *st1 = lds + L::A_BYTES, *st2 = lds + 2 * L::A_BYTES, *st3 = lds + 3 * L::A_BYTES;
     int tm, tn;
     tile_of(gm, gn, &tm, &tn);
     const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
@@ -747,7 +745,8 @@ residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
-    dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, 0, nk, st0, st1, st2, st3, acc);
+    if constexpr (PF) dl_mainloop_pf<BM, BN, WM, WN>(A, B, m0, n0, 0, nk, st0, st1, st2, st3, acc);
+    else dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, 0, nk, st0, st1, st2, st3, acc);
     const int p = crt_mod[l];
     const double invp = crt_invp[l];
     uint8_t *y = R.y + (uint64_t)l * R.y_plane;
@@ -1096,8 +1095,18 @@ static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, 
         Opnd B{bp, 1, (int64_t)L.np, n};
         ResOut R{y, L.y_plane, L.a_plane, L.b_plane, h};
         const int gm = (int)((m + BM - 1) / BM), gn = (int)((n + BN - 1) / BN);
-        hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4>), dim3((unsigned)(gm * gn), 1, (unsigned)nm),
-                           dim3(512), 0, s, A, B, L.kp, gm, gn, R);
+        const dim3 grid((unsigned)(gm * gn), 1, (unsigned)nm);
+        switch (dl_variant()) {
+        case DL_W4:
+            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 2, false>), grid, dim3(256), 0, s, A, B, L.kp, gm, gn, R);
+            break;
+        case DL_W8PF:
+            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, true>), grid, dim3(512), 0, s, A, B, L.kp, gm, gn, R);
+            break;
+        default:
+            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, false>), grid, dim3(512), 0, s, A, B, L.kp, gm, gn, R);
+            break;
+        }
     }
     // 5. reconstruction, epilogue, encode.
     {

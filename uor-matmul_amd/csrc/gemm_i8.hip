@@ -421,17 +421,14 @@ gemm_i8_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm,
 
 // WM x WN waves of 64 lanes (4 waves: one per SIMD, 128x128 each at BM=BN=256;
 // 8 waves: two per SIMD, so one wave's LDS reads overlap the other's MFMAs).
-template <int BM, int BN, int WM, int WN, int EPI, bool FAST, int OB>
+template <int BM, int BN, int WM, int WN, int EPI, bool FAST, int OB, bool PF>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
 gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm, int gn) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     using L = DlLayout<BM, BN>;
-    static_assert(WM * WN * (32 * 33) * 4 <= 2 * L::STAGE, "epilogue parking fits two stages");
-    // One LDS object per stage, so that every read names the stage it reads.
-    __shared__ __attribute__((aligned(16))) char st0[L::STAGE];
-    __shared__ __attribute__((aligned(16))) char st1[L::STAGE];
-    __shared__ __attribute__((aligned(16))) char st2[L::STAGE];
-    __shared__ __attribute__((aligned(16))) char st3[L::STAGE];
+    static_assert(WM * WN * (32 * 33) * 4 <= L::BYTES, "epilogue parking fits the stages");
+    __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
+    char *st0 = lds, *st1 = lds + L::A_BYTES, *st2 = lds + 2 * L::A_BYTES, *st3 = lds + 3 * L::A_BYTES;
 
     int tm, tn;
     tile_of(gm, gn, &tm, &tn);
@@ -453,7 +450,8 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
-    dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc);
+    if constexpr (PF) dl_mainloop_pf<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc);
+    else dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc);
     __syncthreads();
 
     if constexpr (EPI == EPI_FUSED && FAST && OB <= 4 && WM * WN == 8 && FM * FN == 8) {
@@ -461,8 +459,121 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
         // (16 KiB, row stride 32 ints with the column XOR-swizzled by row bit
         // 2 against bank conflicts) and loads their 64 C values per lane in
         // one batch, so a tile costs two memory round trips per wave.
-        char *region = wave < 2 ? st0 : wave < 4 ? st1 : wave < 6 ? st2 : st3;
-        int *park4 = (int *)(region + (wave & 1) * 16384);
+        static_assert(WM * WN * 16384 <= L::BYTES, "16 KiB of parking per wave");
+        int *park4 = (int *)(lds + wave * 16384);
+        // i32 output with unit column stride and 16-byte rows: each lane
+        // takes four consecutive columns of a parked block, so C moves in
+        // 16-byte loads and stores (8 lanes per 128-byte row segment).
+        const bool vec = OB == 4 && out.cs == 1 && (out.rs & 3) == 0 && (((uintptr_t)out.base & 15) == 0);
+        if constexpr (OB == 4) {
+            // A full tile with beta != 0: stream C's 256 rows into the free
+            // stages by LDS DMA (two halves of 128 rows, 1 KiB per row, one
+            // wave instruction per row) so a CU keeps 128 KiB of C in
+            // flight, then combine each accumulator with its prior in place.
+            if (vec && out.beta != 0 && m0 + BM <= A.mn && n0 + BN <= B.mn) {
+                static_assert(BN == 256 && BM == 256 && L::BYTES >= 128 * 1024, "one 1 KiB row per wave load");
+                const int32_t *cbase = (const int32_t *)out.base + (int64_t)m0 * out.rs + (int64_t)n0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    // Rows 128h + 16 * wave + u, u < 16: row r lands at lds + 1024 * (r - 128h).
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) {
+                        const int r = 16 * wave + u;
+                        lds_dma16((const int8_t *)(cbase + (int64_t)(128 * h + r) * out.rs) + 16 * lane,
+                                  lds + 1024 * r);
+                    }
+                    wait_vm<0>();
+                    __syncthreads();
+                    if (wm == h) {
+#pragma unroll
+                        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                            for (int j = 0; j < FN; ++j) {
+                                const int cl = wn * (BN / WN) + 32 * j + l32;
+#pragma unroll
+                                for (int r = 0; r < 16; ++r) {
+                                    const int rl = 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);  // row within the half
+                                    const int64_t prior = ((const int32_t *)lds)[rl * 256 + cl];
+                                    const int64_t x = (int64_t)acc[i][j][r] * out.alpha + prior * out.beta;
+                                    ((int32_t *)out.base)[(int64_t)(m0 + 128 * h + rl) * out.rs + (int64_t)(n0 + cl)] =
+                                        (int32_t)encode_int((i128)x, 4, out.mode);
+                                }
+                            }
+                        }
+                    }
+                    __syncthreads();
+                }
+                return;
+            }
+            if (vec) {
+                const int rq = lane >> 3, c4 = 4 * (lane & 7);
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    v4i prior[4][4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int i = 2 * g + q / 2, j = q % 2;
+                        const uint64_t col = n0 + wn * (BN / WN) + 32 * j + c4;
+                        const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const uint64_t row = rbase + 8 * t + rq;
+                            prior[q][t] = v4i{};
+                            if (out.beta == 0 || row >= A.mn) continue;
+                            const int32_t *cp = (const int32_t *)out.base + (int64_t)row * out.rs + (int64_t)col;
+                            if (col + 3 < B.mn) {
+                                prior[q][t] = *(const v4i *)cp;
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    if (col + e < B.mn) prior[q][t][e] = cp[e];
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int i = 2 * g + q / 2, j = q % 2;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+                            park4[q * 1024 + row * 32 + (l32 ^ (((row >> 2) & 1) << 4))] = acc[i][j][r];
+                        }
+                    }
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int i = 2 * g + q / 2, j = q % 2;
+                        const uint64_t col = n0 + wn * (BN / WN) + 32 * j + c4;
+                        const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const int lr = 8 * t + rq;
+                            const uint64_t row = rbase + lr;
+                            if (row >= A.mn || col >= B.mn) continue;
+                            const v4i sum = *(const v4i *)&park4[q * 1024 + lr * 32 + (c4 ^ (((lr >> 2) & 1) << 4))];
+                            v4i res;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                int64_t x = (int64_t)sum[e] * out.alpha;
+                                if (out.beta != 0) x += (int64_t)prior[q][t][e] * out.beta;
+                                res[e] = (int32_t)encode_int((i128)x, 4, out.mode);
+                            }
+                            int32_t *cp = (int32_t *)out.base + (int64_t)row * out.rs + (int64_t)col;
+                            if (col + 3 < B.mn) {
+                                *(v4i *)cp = res;
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    if (col + e < B.mn) cp[e] = res[e];
+                            }
+                        }
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                }
+                return;
+            }
+        }
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
             // Blocks q = 0..3 of this batch are (i, j) = (2g + q/2, q%2).
@@ -515,8 +626,7 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
         return;
     }
 
-    // Waves 0..3 park in stage 0, waves 4..7 in stage 1.
-    int *park = (int *)(wave < 4 ? st0 : st1) + (wave & 3) * (32 * 33);
+    int *park = (int *)lds + wave * (32 * 33);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -573,16 +683,16 @@ static hipError_t launch_tile(const Opnd &A, const Opnd &B, const OutArgs &out, 
 }
 
 
-template <int BM, int BN, int WM, int WN, int EPI, bool FAST>
+template <int BM, int BN, int WM, int WN, int EPI, bool FAST, bool PF = false>
 static hipError_t launch_dl(const Opnd &A, const Opnd &B, const OutArgs &out, uint64_t K,
                             uint64_t kslice, int splits, hipStream_t s) {
-    auto kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 4>;
+    auto kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 4, PF>;
     if constexpr (EPI != EPI_PARTIAL) {
         switch (out.ob) {
-        case 1: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 1>; break;
-        case 2: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 2>; break;
-        case 8: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 8>; break;
-        case 16: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, false, 16>; break;
+        case 1: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 1, PF>; break;
+        case 2: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 2, PF>; break;
+        case 8: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 8, PF>; break;
+        case 16: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, false, 16, PF>; break;
         default: break;
         }
     }
@@ -595,16 +705,6 @@ static hipError_t launch_dl(const Opnd &A, const Opnd &B, const OutArgs &out, ui
 // The direct-to-LDS pipeline applies when both operands stream in 16-byte
 // chunks along their contiguous axes and every chunk is whole: k a multiple
 // of its 64-byte step (of the split slice too) and n of 16.
-// Which 256x256 pipeline runs (UOR_GFX950_DL_VARIANT = w8 | w4 at load time;
-// w8 by default): 8 waves (two per SIMD) or 4 waves (one per SIMD).
-static int dl_variant() {
-    static int v = [] {
-        const char *e = getenv("UOR_GFX950_DL_VARIANT");
-        return (e && !strcmp(e, "w4")) ? 4 : 8;
-    }();
-    return v;
-}
-
 static bool dl_ok(int pair, uint64_t K, uint64_t N) {
     return pair == 0 && K % DL_BK == 0 && N % 16 == 0;
 }
@@ -759,10 +859,11 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
     int bm;
     if (t256 >= 256 && dl_ok(pair, K, N)) {
         bm = 256;
-        if (dl_variant() == 4)
-            UOR_HIP((launch_dl<256, 256, 2, 2, EPI_FUSED, FAST>(A, B, out, K, 0, 1, s)));
-        else
-            UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST>(A, B, out, K, 0, 1, s)));
+        switch (dl_variant()) {
+        case DL_W4: UOR_HIP((launch_dl<256, 256, 2, 2, EPI_FUSED, FAST, false>(A, B, out, K, 0, 1, s))); break;
+        case DL_W8PF: UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST, true>(A, B, out, K, 0, 1, s))); break;
+        default: UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST, false>(A, B, out, K, 0, 1, s))); break;
+        }
         if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline
     } else if (FAST && t256 >= 256 && pair != 4) {
         // (The i128 epilogue does not fit beside a 256-wide generic tile's

@@ -3,9 +3,27 @@
 // tile order, the LDS stage layout, and the four-stage k loop.
 #pragma once
 
+#include <stdlib.h>
+#include <string.h>
+
 #include "common.hpp"
 
 namespace uor {
+
+// Which 256x256 pipeline runs (UOR_GFX950_DL_VARIANT at load time): 8 waves
+// (two per SIMD) with the first half of each step's fragments prefetched one
+// step ahead (w8pf, the default), the same without the prefetch (w8), or 4
+// waves (one per SIMD, w4).  All give the same bytes.
+enum : int { DL_W8 = 0, DL_W4 = 1, DL_W8PF = 2 };
+static inline int dl_variant() {
+    static int v = [] {
+        const char *e = getenv("UOR_GFX950_DL_VARIANT");
+        if (e && !strcmp(e, "w8")) return (int)DL_W8;
+        if (e && !strcmp(e, "w4")) return (int)DL_W4;
+        return (int)DL_W8PF;
+    }();
+    return v;
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -62,12 +80,18 @@ typedef __attribute__((address_space(3))) void lds_void;
 constexpr int DL_BK = 64;
 constexpr int DL_NSTAGE = 4;
 
+// One LDS array per workgroup: the A halves of all stages first, then the B
+// halves, so that a stage handle (its A half) reaches its B half at a fixed
+// offset and every fragment read is a lane base plus an immediate offset
+// (DS offsets are 16 bits: the four 16 KiB A halves fit below 64 KiB).
 template <int BM, int BN>
 struct DlLayout {
+    static_assert(BM == BN, "the B halves sit one A region above their A halves");
     static constexpr int A_BYTES = BM * DL_BK;
     static constexpr int B_BYTES = BN * DL_BK;
     static constexpr int STAGE = A_BYTES + B_BYTES;
     static constexpr int BYTES = DL_NSTAGE * STAGE;
+    static constexpr int B_OFF = DL_NSTAGE * A_BYTES;  // stage handle -> its B half
     __device__ static inline int a_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
     __device__ static inline int b_swz(int k) { return (2 * (k & 7)) & (BN / 16 - 1); }
     __device__ static inline int b_off(int k, int x) { return k * BN + 16 * (x ^ b_swz(k)); }
@@ -132,7 +156,7 @@ __device__ inline void dl_issue(const Opnd &A, const Opnd &B, uint64_t m0, uint6
         lds_dma16(A.base + (int64_t)gr * A.s_mn + (int64_t)(k0 + 16 * c), stage + base * 16);
     }
     // B: BN/16 chunks per k-row, slot s = k*(BN/16) + physical chunk.
-    char *bst = stage + L::A_BYTES;
+    char *bst = stage + L::B_OFF;
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
         const int base = (wave * PB + i) * 64;
@@ -184,7 +208,7 @@ __device__ inline void dl_compute(const char *sa, const char *sb,
 }
 
 // The k loop over nk steps of DL_BK from kbeg: each wave's FM x FN 32x32
-// accumulators, stages st0..st3 (distinct LDS objects of the caller).  Ends
+// accumulators, stage handles st0..st3 (A halves; B halves at B_OFF above).  Ends
 // with every load retired; the caller's barrier then frees the stages.
 template <int BM, int BN, int WM, int WN>
 __device__ inline void dl_mainloop(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0,
@@ -209,7 +233,7 @@ __device__ inline void dl_mainloop(const Opnd &A, const Opnd &B, uint64_t m0, ui
         stage_barrier();                                                                       \
         if (kt + DL_NSTAGE - 1 < nk)                                                           \
             dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + (uint64_t)(kt + DL_NSTAGE - 1) * DL_BK, NXT); \
-        dl_compute<BM, BN, WM, WN>(CUR, CUR + L::A_BYTES, acc);                                \
+        dl_compute<BM, BN, WM, WN>(CUR, CUR + L::B_OFF, acc);                                \
         if (++kt >= nk) break;                                                                 \
     }
     for (int kt = 0; kt < nk;) {
@@ -219,6 +243,109 @@ __device__ inline void dl_mainloop(const Opnd &A, const Opnd &B, uint64_t m0, ui
         UOR_DL_STEP(st3, st2)
     }
 #undef UOR_DL_STEP
+    wait_vm<0>();
+}
+
+// ---------------------------------------------- half-prefetch variant --
+//
+// The same stages and loads.  Each 64-deep step is two 32-deep halves: the
+// first half's fragments (f0) are read during the previous step, so the
+// step's MFMAs start as soon as its barrier passes; the second half's (f1)
+// are read right after the barrier and arrive while the first half's MFMAs
+// run; then the next step's first half is read into f0.  Register use is the
+// same as reading both halves in-step.  A stage's last reads happen in its
+// own step, so step t's barrier frees stage t-1, which takes step t+3.
+
+template <int BM, int BN, int WM, int WN>
+struct DlHalf {
+    static constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    v4i a[FM];
+    v4i b[FN];
+};
+
+template <int BM, int BN, int WM, int WN>
+__device__ inline void dl_read_half(const char *sa, const char *sb, int ks,
+                                    DlHalf<BM, BN, WM, WN> &f) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    using L = DlLayout<BM, BN>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int half = lane >> 5, l32 = lane & 31;
+    const int grp = lane >> 4, t16 = lane & 15;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+        f.a[i] = *(const v4i *)(sa + L::a_off(wm * (BM / WM) + 32 * i + l32, 2 * ks + half));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int nb = wn * (BN / WN) + 32 * j + 16 * (grp & 1) + 8 * (t16 & 1);
+        const int k = 32 * ks + 16 * (grp >> 1) + (t16 >> 1);
+        v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(sb + L::b_off(k, nb >> 4) + (nb & 8)));
+        v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(sb + L::b_off(k + 8, nb >> 4) + (nb & 8)));
+        f.b[j] = v4i{lo[0], lo[1], hi[0], hi[1]};
+    }
+}
+
+// MFMAs q0 <= q < q1 of one half, q = i * FN + j.
+template <int BM, int BN, int WM, int WN, int Q0, int Q1>
+__device__ inline void dl_mfma_half(const DlHalf<BM, BN, WM, WN> &f,
+                                    v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
+    constexpr int FN = BN / WN / 32;
+#pragma unroll
+    for (int q = Q0; q < Q1; ++q)
+        acc[q / FN][q % FN] =
+            __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[q / FN], f.b[q % FN], acc[q / FN][q % FN], 0, 0, 0);
+}
+
+template <int BM, int BN, int WM, int WN>
+__device__ inline void dl_mainloop_pf(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0,
+                                      uint64_t kbeg, int nk, char *st0, char *st1, char *st2,
+                                      char *st3, v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
+    constexpr int NT = 64 * WM * WN;
+    using L = DlLayout<BM, BN>;
+    constexpr int LOADS = (BM + BN) * 4 / NT;  // global_load_lds per thread per stage
+    static_assert(DL_NSTAGE == 4, "the k loop below is unrolled by four stages");
+    static_assert(DL_BK == 64, "two 32-deep halves per step");
+    if (nk <= 0) return;
+    DlHalf<BM, BN, WM, WN> f0, f1;
+    dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg, st0);
+    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + DL_BK, st1);
+    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + 2 * DL_BK, st2);
+    {
+        const int later = min(2, nk - 1);
+        if (later >= 2) wait_vm<2 * LOADS>();
+        else if (later == 1) wait_vm<LOADS>();
+        else wait_vm<0>();
+    }
+    stage_barrier();
+    dl_read_half<BM, BN, WM, WN>(st0, st0 + L::B_OFF, 0, f0);
+
+    // Step t: CUR = stage t, NXT = stage t+1, FREE = stage t-1 (= t+3).
+    // The empty asm statement (a compiler memory barrier) keeps the next f0
+    // reads behind the first-half MFMAs.
+    constexpr int NQ = DlHalf<BM, BN, WM, WN>::FM * DlHalf<BM, BN, WM, WN>::FN;
+#define UOR_DL_PF_STEP(CUR, NXT, FREE)                                                        \
+    {                                                                                          \
+        if (kt + 1 < nk) {                                                                     \
+            if (kt + 2 < nk) wait_vm<LOADS>();                                                 \
+            else wait_vm<0>();                                                                 \
+        }                                                                                      \
+        stage_barrier();                                                                       \
+        dl_read_half<BM, BN, WM, WN>(CUR, CUR + L::B_OFF, 1, f1);                               \
+        dl_mfma_half<BM, BN, WM, WN, 0, NQ / 2>(f0, acc);                                      \
+        if (kt + 3 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + (uint64_t)(kt + 3) * DL_BK, FREE); \
+        dl_mfma_half<BM, BN, WM, WN, NQ / 2, NQ>(f0, acc);                                     \
+        asm volatile("" ::: "memory");                                                         \
+        if (kt + 1 < nk) dl_read_half<BM, BN, WM, WN>(NXT, NXT + L::B_OFF, 0, f0);              \
+        dl_mfma_half<BM, BN, WM, WN, 0, NQ>(f1, acc);                                          \
+        if (++kt >= nk) break;                                                                 \
+    }
+    for (int kt = 0; kt < nk;) {
+        UOR_DL_PF_STEP(st0, st1, st3)
+        UOR_DL_PF_STEP(st1, st2, st0)
+        UOR_DL_PF_STEP(st2, st3, st1)
+        UOR_DL_PF_STEP(st3, st0, st2)
+    }
+#undef UOR_DL_PF_STEP
     wait_vm<0>();
 }
 
