@@ -809,7 +809,11 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
     // exceeds one i32 lane.
     const bool want_split = (K > (uint64_t)KCHUNK) || (t64 < 256 && K >= 8192);
     if (want_split && have_work) {
-        const int BMN = t128 >= 64 ? 128 : 64;
+        // The 128-wide direct-to-LDS tile whenever its layout applies (it
+        // streams whole 128-byte B rows, which matters most for the deep,
+        // HBM-bound shapes), else 128 or 64 by the tile count.
+        const bool dl128 = dl_ok(pair, K, N);
+        const int BMN = (t128 >= 64 || dl128) ? 128 : 64;
         const uint64_t tiles = BMN == 128 ? t128 : t64;
         uint64_t splits = (1024 + tiles - 1) / tiles;
         uint64_t min_splits = (K + KCHUNK - 1) / KCHUNK;
@@ -825,7 +829,7 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         hipLaunchKernelGGL(zero_i64_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s,
                            out.work, cells);
         UOR_HIP(hipGetLastError());
-        if (BMN == 128 && dl_ok(pair, K, N) && kslice % DL_BK == 0)
+        if (BMN == 128 && dl128 && kslice % DL_BK == 0)
             UOR_HIP((launch_dl<128, 128, 2, 2, EPI_PARTIAL, FAST>(A, B, out, K, kslice, (int)splits, s)));
         else if (BMN == 128)
             UOR_HIP((launch_modes<128, 128, 128, EPI_PARTIAL, FAST>(pair, A, B, out, K, kslice, (int)splits, s)));
