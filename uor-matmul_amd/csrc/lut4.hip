@@ -21,6 +21,10 @@
 // the codes dominate at decode shapes, so the kernels are built to stream
 // them: every code byte is read from HBM exactly once.
 
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include <type_traits>
 
 #include "common.hpp"
@@ -260,6 +264,110 @@ __global__ void __launch_bounds__(256) lut4_dot4_kernel(LutArgs L, int book_alig
     }
 }
 
+// The same decode, software-pipelined for k <= LUT_SEG: one column per step,
+// with the code chunks and codebooks of the next two columns requested
+// before the current one is decoded (a ring of three register buffers,
+// unrolled by three so nothing is copied), so a wave keeps two columns (8 KiB)
+// of codes in flight.  The activations, the same for every column, sit in
+// LDS (MR x 8 KiB per workgroup, in the decode's order, lane-contiguous).
+template <int MR, bool FAST>
+__global__ void __launch_bounds__(256) lut4_dot4_pf_kernel(LutArgs L, int book_aligned) {
+    __shared__ uint32_t act[MR][4][4][2][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint64_t wave = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint64_t nwaves = ((uint64_t)gridDim.x * blockDim.x) >> 6;
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+
+    // The block's four waves fill the activation table together.
+    for (int q = wv; q < MR * 16; q += 4) {
+        const int r = q / 16, c = (q / 4) % 4, d = q % 4;
+        uint32_t e, o;
+        act8(L, r, (uint64_t)(64 * c + lane) * 32 + 8 * d, FAST, e, o);
+        act[r][c][d][0][lane] = e;
+        act[r][c][d][1][lane] = o;
+    }
+    __syncthreads();
+
+    struct Col {
+        uint4 cw[4];
+        uint32_t q[4];
+    };
+    auto fetch = [&](uint64_t jf, Col &b) {
+        load_book(L, jf, book_aligned, b.q[0], b.q[1], b.q[2], b.q[3]);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) b.cw[cc] = code_chunk<FAST>(L, jf, (uint64_t)(64 * cc + lane) * 16);
+    };
+    typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+    auto compute = [&](uint64_t jc, const Col &b) {
+        // The table's address passes through an empty asm each step, so the
+        // compiler reads it from LDS per use instead of holding all of it in
+        // registers across the loop.
+        uint32_t abase = (uint32_t)(uintptr_t)(lds_u32 *)&act[0][0][0][0][lane];
+        asm volatile("" : "+v"(abase));
+        lds_u32 *ap = (lds_u32 *)(uintptr_t)abase;
+        uint32_t qs[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qs[e] = __builtin_amdgcn_readfirstlane(b.q[e]);
+        int acc[MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[r] = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t w = d == 0 ? b.cw[c].x : d == 1 ? b.cw[c].y : d == 2 ? b.cw[c].z : b.cw[c].w;
+                uint32_t e, o;
+                decode8(w, qs[0], qs[1], qs[2], qs[3], m4, id, e, o);
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    acc[r] = __builtin_amdgcn_sdot4((int)e, (int)ap[(((r * 4 + c) * 4 + d) * 2 + 0) * 64], acc[r], false);
+                    acc[r] = __builtin_amdgcn_sdot4((int)o, (int)ap[(((r * 4 + c) * 4 + d) * 2 + 1) * 64], acc[r], false);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const int sum = wave_sum(acc[r]);
+            if (lane == r && (uint64_t)r < L.m) lut_finish_any(L, r, jc, sum);
+        }
+    };
+    Col b0, b1, b2;
+    uint64_t j = wave;
+    if (j < L.n) fetch(j, b0);
+    if (j + nwaves < L.n) fetch(j + nwaves, b1);
+#define UOR_LUT_STEP(CUR, NN)                                    \
+    {                                                            \
+        if (j + 2 * nwaves < L.n) fetch(j + 2 * nwaves, NN);     \
+        compute(j, CUR);                                         \
+        j += nwaves;                                             \
+        if (j >= L.n) break;                                     \
+    }
+    while (j < L.n) {
+        UOR_LUT_STEP(b0, b2)
+        UOR_LUT_STEP(b1, b0)
+        UOR_LUT_STEP(b2, b1)
+    }
+#undef UOR_LUT_STEP
+}
+
+// Resident blocks of a kernel on the whole device (one persistent round).
+template <typename K>
+static unsigned resident_blocks(K kern) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1024;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1024;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, 256, 0) != hipSuccess || per < 1) per = 1;
+    return (unsigned)(per * cus);
+}
+
+static int lut_variant() {
+    static int v = [] {
+        const char *e = getenv("UOR_GFX950_LUT_VARIANT");
+        return (e && e[0] == 'b') ? 0 : 1;  // "base": no pipelining
+    }();
+    return v;
+}
+
 // --------------------------------------- m > 4: decoded weights into MFMA
 //
 // A workgroup of 4 waves owns a 32-row x 32-column output tile; wave w sums
@@ -387,7 +495,20 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         const uint64_t waves = n < 4096 ? n : 4096;
         const unsigned blocks = (unsigned)((waves + 3) / 4);
         if (route) route->tile_m = m <= 1 ? 1 : m <= 2 ? 2 : 4, route->tile_n = 1;
-        if (fast) {
+        const bool pf = lut_variant() == 1 && k <= (uint64_t)LUT_SEG;
+        if (pf) {
+            // One resident round of the pipelined kernel (its register use
+            // sets how many blocks a CU holds), capped by the columns.
+            auto kern = fast ? (m <= 1 ? lut4_dot4_pf_kernel<1, true> : m <= 2 ? lut4_dot4_pf_kernel<2, true>
+                                                                                  : lut4_dot4_pf_kernel<4, true>)
+                             : (m <= 1 ? lut4_dot4_pf_kernel<1, false> : m <= 2 ? lut4_dot4_pf_kernel<2, false>
+                                                                                   : lut4_dot4_pf_kernel<4, false>);
+            static unsigned cap[2][3] = {{0, 0, 0}, {0, 0, 0}};
+            unsigned &cp = cap[fast ? 1 : 0][m <= 1 ? 0 : m <= 2 ? 1 : 2];
+            if (!cp) cp = resident_blocks(kern);
+            const unsigned pblocks = (unsigned)std::min<uint64_t>(cp, (n + 3) / 4);
+            hipLaunchKernelGGL(kern, dim3(pblocks), dim3(256), 0, s, L, book_aligned);
+        } else if (fast) {
             if (m <= 1) hipLaunchKernelGGL((lut4_dot4_kernel<1, true>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
             else if (m <= 2) hipLaunchKernelGGL((lut4_dot4_kernel<2, true>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
             else hipLaunchKernelGGL((lut4_dot4_kernel<4, true>), dim3(blocks), dim3(256), 0, s, L, book_aligned);
