@@ -450,7 +450,7 @@ static hipError_t launch_direct(const FArgs &F, hipStream_t s) {
 
 // --------------------------------------------------------- CRT route --
 
-constexpr int WIDE_BITS = 160;  // wider lines take the direct loop
+constexpr int WIDE_BITS = 160;  // the widest slice (2W + log2(k S) fits 49 moduli)
 constexpr int CRT_BK_MAX = 1 << 17;  // i32 MFMA sums stay exact: 2^14 * k < 2^31
 
 enum : int32_t { LS_DIRTY = 1, LS_WIDE = 2, LS_EMPTY = 4 };
@@ -465,8 +465,10 @@ struct LineStat {
 struct CrtHdr {
     int32_t nmod;     // moduli in use (0: no residue work)
     int32_t crt_off;  // 1: every cell takes the direct loop
-    int32_t need;     // the bound B used: |X| < 2^B
-    int32_t pad[61];
+    int32_t need;     // the bound B used: |X| < 2^B (per diagonal when sliced)
+    int32_t sa, sb;   // slices per A row / B column (1: unsliced)
+    int32_t w;        // slice width in bits (sliced plans)
+    int32_t pad[58];
 };
 
 // The trimmed significand and exponent of a finite nonzero: m odd.
@@ -565,23 +567,29 @@ __global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64
     }
 }
 
-// The plan: the bound B (|X_ij| < 2^B for every CRT cell) and the fewest
-// moduli whose capacity covers it; crt_off when the offer holds fewer planes.
+// The plan, on the device.  Unsliced (every line at most WIDE_BITS wide): the
+// bound B (|X_ij| < 2^B for every cell) from the line widths and L1 bounds.
+// Sliced: every aligned integer is cut into S slices of W bits, X =
+// sum_{s,t} 2^{W(s+t)} alpha^(s) beta^(t), and the slice pairs of one diagonal
+// d = s + t form one GEMM, whose sum is below min(S_A, S_B) * k * 2^(2W).
+// Then the fewest moduli whose capacity covers B; crt_off when the offer
+// holds fewer planes or slices than the data needs.
 __global__ void __launch_bounds__(256) crt_plan_kernel(const LineStat *ra, uint64_t m,
                                                        const LineStat *cb, uint64_t n, uint64_t k,
-                                                       int nm_alloc, CrtHdr *h) {
+                                                       int nm_alloc, int sa_cap, int sb_cap,
+                                                       CrtHdr *h) {
     __shared__ float s_w[4][256];
     const int t = threadIdx.x;
     float wa = -1e30f, la = -1e30f, wb = -1e30f, lb = -1e30f;
     for (uint64_t i = t; i < m; i += 256) {
         const LineStat s = ra[i];
-        if (s.flags & (LS_WIDE | LS_EMPTY)) continue;
+        if (s.flags & LS_EMPTY) continue;
         wa = fmaxf(wa, (float)s.width);
         la = fmaxf(la, s.l1);
     }
     for (uint64_t j = t; j < n; j += 256) {
         const LineStat s = cb[j];
-        if (s.flags & (LS_WIDE | LS_EMPTY)) continue;
+        if (s.flags & LS_EMPTY) continue;
         wb = fmaxf(wb, (float)s.width);
         lb = fmaxf(lb, s.l1);
     }
@@ -601,19 +609,40 @@ __global__ void __launch_bounds__(256) crt_plan_kernel(const LineStat *ra, uint6
     wb = s_w[2][0];
     lb = s_w[3][0];
     CrtHdr r{};
-    if (wa < 0 || wb < 0) {  // no CRT cell has a nonzero product
-        r.nmod = 0;
-        r.need = 0;
-    } else {
-        int lk = 0;
-        while ((1ull << lk) < k) ++lk;
+    r.sa = r.sb = 1;
+    if (wa < 0 || wb < 0) {  // no cell has a nonzero product
+        *h = r;
+        return;
+    }
+    int lk = 0;
+    while ((1ull << lk) < k) ++lk;
+    int need;
+    if (wa <= WIDE_BITS && wb <= WIDE_BITS) {
         const double b = fmin(fmin((double)la + wb, (double)wa + lb), (double)wa + wb + lk);
-        const int need = (int)ceil(b + 1e-5);
-        int nm = 0;
-        while (nm < CRT_NMAX && crt_cap[nm] < need) ++nm;
-        r.need = need;
-        if (crt_cap[nm] < need || nm > nm_alloc) r.crt_off = 1;
-        else r.nmod = nm;
+        need = (int)ceil(b + 1e-5);
+    } else {
+        const int iwa = (int)wa, iwb = (int)wb;
+        int sa = (iwa + WIDE_BITS - 1) / WIDE_BITS, sb = (iwb + WIDE_BITS - 1) / WIDE_BITS;
+        if (sa < 1) sa = 1;
+        if (sb < 1) sb = 1;
+        const int w = max((iwa + sa - 1) / sa, (iwb + sb - 1) / sb);
+        sa = max(1, (iwa + w - 1) / w);
+        sb = max(1, (iwb + w - 1) / w);
+        int ls = 0;
+        while ((1 << ls) < min(sa, sb)) ++ls;
+        need = 2 * w + lk + ls;
+        r.sa = sa;
+        r.sb = sb;
+        r.w = w;
+    }
+    int nm = 0;
+    while (nm < CRT_NMAX && crt_cap[nm] < need) ++nm;
+    r.need = need;
+    if (crt_cap[nm] < need || nm > nm_alloc || r.sa > sa_cap || r.sb > sb_cap) {
+        r.crt_off = 1;
+        r.nmod = 0;
+    } else {
+        r.nmod = nm;
     }
     *h = r;
 }
@@ -658,79 +687,119 @@ __device__ inline int residue(uint64_t m, int s, bool neg, int l, const uint8_t 
     return b;
 }
 
-// Residue planes: plane l holds prows x ldp bytes; element (r, c) of the
-// source (r < rows, c < cols) at src + r * s_r + c * s_c, its line statistics
-// at st[STAT_ROW ? r : c].  Each thread writes 4 consecutive bytes of a plane
-// row per step of a grid-stride loop; padding (r >= rows or c >= cols) is zero.
-template <bool F64, bool STAT_ROW>
+// Residue planes.  A (ROWS_A): plane l holds m rows of S_A max * kp bytes,
+// slice s of row i at columns [s * kp, s * kp + k).  B: plane l holds
+// S_B max * kp rows of np bytes, slice t at rows [(S_B max - 1 - t) * kp, ...)
+// (reversed, so that the slice pairs of one diagonal are one contiguous k
+// range of both operands).  Padding (k <= p < kp, j >= n) is zero.  Element
+// (r, c) of the source is at src + r * s_r + c * s_c, its line statistics at
+// st[ROWS_A ? r : c].  Each thread writes 4 consecutive plane bytes per step
+// of a grid-stride loop over the slices the plan uses.
+template <bool F64, bool ROWS_A>
 __global__ void __launch_bounds__(256) residue_kernel(const char *src, int64_t s_r, int64_t s_c,
-                                                      uint64_t rows, uint64_t cols, uint64_t prows,
-                                                      uint64_t ldp, const LineStat *st,
+                                                      uint64_t rows, uint64_t cols, uint64_t kp,
+                                                      uint64_t np, int s_max, const LineStat *st,
                                                       const CrtHdr *h, int8_t *planes,
                                                       uint64_t plane_bytes) {
     __shared__ uint32_t pow2w[CRT_NMAX * 64];
     const int nmod = h->nmod;
+    const int ns = ROWS_A ? h->sa : h->sb;
+    const int w = (h->sa > 1 || h->sb > 1) ? h->w : 0;  // 0: unsliced
     const uint32_t *tab = (const uint32_t *)&crt_pow2[0][0];
     for (int q = threadIdx.x; q < nmod * 64; q += 256) pow2w[q] = tab[q];
     __syncthreads();
     if (nmod == 0) return;
     const uint8_t *pow2 = (const uint8_t *)pow2w;
-    const uint64_t chunks = ldp / 4, total = prows * chunks;
+    // Logical chunk space: (slice, R, C / 4) with (R, C) = (m, kp) for A and
+    // (kp, np) for B; source coordinates (row, col) follow.
+    const uint64_t R = ROWS_A ? rows : kp, C = ROWS_A ? kp : np;
+    const uint64_t chunks = C / 4, per_slice = R * chunks, total = (uint64_t)ns * per_slice;
     for (uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
          idx += (uint64_t)gridDim.x * 256) {
-        const uint64_t r = idx / chunks, c0 = (idx % chunks) * 4;
+        const int sl = (int)(idx / per_slice);
+        const uint64_t rem = idx % per_slice;
+        const uint64_t r = rem / chunks, c0 = (rem % chunks) * 4;
         uint64_t mm[4];
         int ss[4];
         bool ok[4], ng[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint64_t c = c0 + e;
+            // Source element: A (r, c0 + e), B (p = r, j = c0 + e).
+            const uint64_t sr = r, sc = c0 + e;
             ok[e] = false;
             ng[e] = false;
             mm[e] = 0;
             ss[e] = 0;
-            if (r >= rows || c >= cols) continue;
-            const LineStat ls = st[STAT_ROW ? r : c];
-            if (ls.flags & (LS_WIDE | LS_EMPTY)) continue;
-            const Dec d = decode<F64>(load_bits<F64>(src, (int64_t)r * s_r + (int64_t)c * s_c));
+            if (sr >= rows || sc >= cols) continue;
+            const LineStat ls = st[ROWS_A ? sr : sc];
+            if (ls.flags & LS_EMPTY) continue;
+            const Dec d = decode<F64>(load_bits<F64>(src, (int64_t)sr * s_r + (int64_t)sc * s_c));
             if (d.cls != CLS_FINITE || !d.mant) continue;
+            uint64_t m;
             int x;
-            trim(d, &mm[e], &x);
-            ss[e] = x - ls.lo;
+            trim(d, &m, &x);
+            const int sh = x - ls.lo;  // the aligned integer is m * 2^sh
+            if (w == 0) {
+                mm[e] = m;
+                ss[e] = sh;
+            } else {
+                // Bits [w * sl, w * (sl + 1)) of m * 2^sh.
+                const int lo_bit = w * sl, hi_bit = lo_bit + w, bl = bitlen64(m);
+                if (sh >= hi_bit || sh + bl <= lo_bit) continue;
+                if (sh >= lo_bit) {
+                    const int keep = hi_bit - sh;  // bits of m inside the slice
+                    mm[e] = keep >= 64 ? m : (m & ((1ull << keep) - 1));
+                    ss[e] = sh - lo_bit;
+                } else {
+                    mm[e] = m >> (lo_bit - sh);  // below 2^53 <= 2^w: no upper mask
+                    ss[e] = 0;
+                }
+                if (!mm[e]) continue;
+            }
             ng[e] = d.neg;
             ok[e] = true;
         }
-        int8_t *dst = planes + r * ldp + c0;
+        int8_t *dst = ROWS_A ? planes + r * ((uint64_t)s_max * kp) + (uint64_t)sl * kp + c0
+                             : planes + ((uint64_t)(s_max - 1 - sl) * kp + r) * np + c0;
         for (int l = 0; l < nmod; ++l) {
-            uint32_t w = 0;
+            uint32_t wd = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int v = ok[e] ? residue<F64>(mm[e], ss[e], ng[e], l, pow2) : 0;
-                w |= (uint32_t)(uint8_t)(int8_t)v << (8 * e);
+                wd |= (uint32_t)(uint8_t)(int8_t)v << (8 * e);
             }
-            *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = w;
+            *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = wd;
         }
     }
 }
 
 struct ResOut {
-    uint8_t *y;  // plane l at y + l * y_plane: m x n bytes, row-major
+    uint8_t *y;  // diagonal d, modulus l at y + (d * nm + l) * y_plane: m x n bytes
     uint64_t y_plane;
-    uint64_t a_plane, b_plane;  // residue plane strides
+    int nm;      // moduli the planes are laid out for
+    int8_t *ap, *bp;  // residue planes: A [l][m][sa_max * kp], B [l][sb_max * kp][np]
+    uint64_t a_plane, b_plane;
+    uint64_t kp, np;
+    int sa_max, sb_max;
     const CrtHdr *h;
 };
 
-// One modulus per grid z: the exact i32 product of its residue planes,
-// reduced mod p into a byte per cell.
+// One (diagonal, modulus) per grid (y, z): the exact i32 sum over the
+// diagonal's slice pairs -- one contiguous k range of both operands -- reduced
+// mod p into a byte per cell.
 template <int BM, int BN, int WM, int WN, bool PF>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
-residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
+residue_gemm_kernel(uint64_t m, uint64_t n, int gm, int gn, ResOut R) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     using L = DlLayout<BM, BN>;
-    const int l = blockIdx.z;
-    if (l >= R.h->nmod) return;
-    A.base += (uint64_t)l * R.a_plane;
-    B.base += (uint64_t)l * R.b_plane;
+    const int d = blockIdx.y, l = blockIdx.z;
+    const CrtHdr hd = *R.h;
+    if (l >= hd.nmod || d >= hd.sa + hd.sb - 1) return;
+    const int a0 = max(0, d - hd.sb + 1), a1 = min(d, hd.sa - 1);
+    const uint64_t K = (uint64_t)(a1 - a0 + 1) * R.kp;
+    Opnd A{R.ap + (uint64_t)l * R.a_plane + (uint64_t)a0 * R.kp, (int64_t)((uint64_t)R.sa_max * R.kp), 1, m};
+    Opnd B{R.bp + (uint64_t)l * R.b_plane + (uint64_t)(R.sb_max - 1 - d + a0) * R.kp * R.np, 1,
+           (int64_t)R.np, n};
     __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
     char *st0 = lds, *st1 = lds + L::A_BYTES, *st2 = lds + 2 * L::A_BYTES, *st3 = lds + 3 * L::A_BYTES;
     int tm, tn;
@@ -749,18 +818,18 @@ residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
     else dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, 0, nk, st0, st1, st2, st3, acc);
     const int p = crt_mod[l];
     const double invp = crt_invp[l];
-    uint8_t *y = R.y + (uint64_t)l * R.y_plane;
+    uint8_t *y = R.y + ((uint64_t)d * R.nm + l) * R.y_plane;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const uint64_t col = n0 + wn * (BN / WN) + 32 * j + l32;
             const uint64_t rbase = m0 + wm * (BM / WM) + 32 * i;
-            if (col >= B.mn) continue;
+            if (col >= n) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint64_t row = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (row >= A.mn) continue;
+                if (row >= m) continue;
                 const int v = acc[i][j][r];
                 int q;
                 if (l == 0) {
@@ -770,7 +839,7 @@ residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
                     if (q < 0) q += p;
                     if (q >= p) q -= p;
                 }
-                y[row * B.mn + col] = (uint8_t)q;
+                y[row * n + col] = (uint8_t)q;
             }
         }
     }
@@ -781,36 +850,44 @@ residue_gemm_kernel(Opnd A, Opnd B, uint64_t K, int gm, int gn, ResOut R) {
 // a residue (< 2^8) and a 16-bit digit of M / p_l, below 2^30, so the sums
 // run on 24-bit multiply-adds in 32-bit lanes; the quotient round(sum c_l /
 // p_l) is exact in a double because |X| / M stays 2^-21 away from 1/2.
-template <int ND>
+template <int ND, int G = 8>
 __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, int nmod,
                              uint32_t (&D)[ND]) {
     int32_t sl[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) sl[d] = 0;
-    // Every plane's byte first, so the loads overlap instead of each waiting.
-    int yb[CRT_NMAX];
-#pragma unroll
-    for (int l = 0; l < CRT_NMAX; ++l) yb[l] = l < nmod ? (int)y[(uint64_t)l * y_plane + cell] : 0;
     double f = 0;
     const uint16_t(*Ml)[CRT_ND16] = crt_Ml16[nmod - 1];
     const uint16_t *inv = crt_inv[nmod - 1];
+    // G planes' bytes at a time, so their loads overlap (all of them where
+    // registers allow).
 #pragma unroll
-    for (int l = 0; l < CRT_NMAX; ++l) {
-        if (l < nmod) {
-            const int p = crt_mod[l];
-            const int prod = yb[l] * (int)inv[l];  // < 2^16
-            int c;
-            if (l == 0) {
-                c = prod & 255;
-            } else {
-                const int q = (int)((float)prod * crt_invpf[l]);
-                c = prod - q * p;
-                if (c < 0) c += p;
-                if (c >= p) c -= p;
+    for (int l0 = 0; l0 < CRT_NMAX; l0 += G) {
+        if (l0 < nmod) {
+            int yb[G];
+#pragma unroll
+            for (int u = 0; u < G; ++u)
+                yb[u] = (l0 + u < CRT_NMAX && l0 + u < nmod) ? (int)y[(uint64_t)(l0 + u) * y_plane + cell] : 0;
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int l = l0 + u;
+                if (l < CRT_NMAX && l < nmod) {
+                    const int p = crt_mod[l];
+                    const int prod = yb[u] * (int)inv[l];  // < 2^16
+                    int c;
+                    if (l == 0) {
+                        c = prod & 255;
+                    } else {
+                        const int q = (int)((float)prod * crt_invpf[l]);
+                        c = prod - q * p;
+                        if (c < 0) c += p;
+                        if (c >= p) c -= p;
+                    }
+                    f += (double)c * crt_invp[l];
+#pragma unroll
+                    for (int d = 0; d < ND; ++d) sl[d] += c * (int32_t)Ml[l][d];
+                }
             }
-            f += (double)c * crt_invp[l];
-#pragma unroll
-            for (int d = 0; d < ND; ++d) sl[d] += c * (int32_t)Ml[l][d];
         }
     }
     const int32_t q = (int32_t)floor(f + 0.5);
@@ -941,71 +1018,105 @@ __device__ inline int flags_cell(const FArgs &F, uint64_t i, uint64_t j) {
     return flags;
 }
 
-// One CRT cell: reconstruct, then either the register epilogue (no flags,
-// |alpha| < 2^16, beta * C zero: the common case) or the digit register in
-// LDS shared with the direct route (everything else).
+// The cells the register epilogue takes: an unsliced plan, no non-finite
+// code on the cell's lines, beta = 0 and 0 < |alpha| < 2^16.  Decided from
+// the plan and the line statistics only (never from C, which the fast kernel
+// overwrites), so the two finish kernels split the cells exactly.
+__device__ inline bool fast_cell(const FArgs &F, const CrtHdr &hd, const LineStat &sa,
+                                 const LineStat &sb) {
+    const uint64_t fa = F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha;
+    return !hd.crt_off && hd.sa == 1 && hd.sb == 1 && !((sa.flags | sb.flags) & LS_DIRTY) &&
+           F.beta == 0 && fa != 0 && fa < 65536;
+}
+
+// The register epilogue of one fast cell: reconstruct, scale by alpha,
+// encode, store.
 template <bool F64, int ND>
-__device__ inline void crt_cell(const FArgs &F, const Reg &R, const LineStat &sa,
-                                const LineStat &sb, int flags, int nmod, const uint8_t *y,
-                                uint64_t y_plane, uint64_t i, uint64_t j) {
-    using Fm = Fmt<F64>;
-    constexpr int S = Fm::DIGITS;
+__device__ inline void crt_fast_cell(const FArgs &F, const LineStat &sa, const LineStat &sb,
+                                     int nmod, const uint8_t *y, uint64_t y_plane, uint64_t i,
+                                     uint64_t j) {
     uint32_t D[ND + 1];
-    D[ND] = 0;
     bool neg = false;
     if (nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY)) {
-        uint32_t X[ND];
-        neg = crt16<ND>(y, y_plane, i * F.n + j, nmod, X);
-#pragma unroll
-        for (int d = 0; d < ND; ++d) D[d] = X[d];
+        neg = crt16<ND + 1, CRT_NMAX>(y, y_plane, i * F.n + j, nmod, D);
     } else {
 #pragma unroll
-        for (int d = 0; d < ND; ++d) D[d] = 0;
+        for (int dd = 0; dd <= ND; ++dd) D[dd] = 0;
     }
-    const int E = sa.lo + sb.lo;
-    const int64_t ci = (int64_t)i * F.crs + (int64_t)j * F.ccs;
-    bool c_zero = true;
-    if (F.beta != 0) {
-        const Dec dc = decode<F64>(load_bits<F64>(F.c, ci));
-        c_zero = dc.cls == CLS_FINITE && dc.mant == 0;
-    }
-    const uint64_t fa = F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha;
-    if (flags == 0 && c_zero && fa != 0 && fa < 65536) {
-        if (fa != 1) {
-            uint32_t carry = 0;
+    const uint32_t fa = (uint32_t)(F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha);
+    if (fa != 1) {
+        uint32_t carry = 0;
 #pragma unroll
-            for (int d = 0; d <= ND; ++d) {
-                const uint32_t v = D[d] * (uint32_t)fa + carry;
-                D[d] = v & 0xffff;
-                carry = v >> 16;
+        for (int dd = 0; dd <= ND; ++dd) {
+            const uint32_t v = D[dd] * fa + carry;
+            D[dd] = v & 0xffff;
+            carry = v >> 16;
+        }
+    }
+    if (F.alpha < 0) neg = !neg;
+    store_bits<F64>(F.c, (int64_t)i * F.crs + (int64_t)j * F.ccs,
+                    encode16<F64, ND + 1>(D, sa.lo + sb.lo, neg, F.mode));
+}
+
+// Every other CRT cell: each diagonal's sum into the digit register (signed
+// digits, so differently signed diagonals cancel exactly; a sliced plan adds
+// diagonal d W * d bits higher), then the epilogue shared with the direct
+// route.
+template <bool F64, int ND>
+__device__ inline void crt_general_cell(const FArgs &F, const Reg &R, const LineStat &sa,
+                                        const LineStat &sb, int flags, const CrtHdr &hd, int nm,
+                                        const uint8_t *y, uint64_t y_plane, uint64_t i, uint64_t j) {
+    using Fm = Fmt<F64>;
+    constexpr int S = Fm::DIGITS;
+    for (int q = 0; q < S; ++q) R[q] = 0;
+    if (hd.nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY)) {
+        const int ndiag = hd.sa + hd.sb - 1;
+        const int E = sa.lo + sb.lo;
+        for (int dg = 0; dg < ndiag; ++dg) {
+            uint32_t X[ND];
+            const bool neg = crt16<ND>(y + (uint64_t)dg * nm * y_plane, y_plane, i * F.n + j, hd.nmod, X);
+            const int pos = E - Fm::RB + hd.w * dg;
+            const int q0 = pos >> 5, r = pos & 31;
+#pragma unroll
+            for (int dd = 0; dd < ND; dd += 2) {
+                const uint32_t pair = X[dd] | ((dd + 1 < ND ? X[dd + 1] : 0u) << 16);
+                if (!pair) continue;
+                const uint64_t wv = (uint64_t)pair << r;
+                const int64_t lo = (int64_t)(wv & M32), hi = (int64_t)(wv >> 32);
+                const int k0 = q0 + dd / 2;
+                if (k0 < S) R[k0] += neg ? -lo : lo;
+                if (k0 + 1 < S) R[k0 + 1] += neg ? -hi : hi;
             }
         }
-        if (F.alpha < 0) neg = !neg;
-        store_bits<F64>(F.c, ci, encode16<F64, ND + 1>(D, E, neg, F.mode));
-        return;
     }
-    // General case: X * 2^E into the digit register, then the shared epilogue.
-    for (int q = 0; q < S; ++q) R[q] = 0;
-    const int pos = E - Fm::RB;
-    const int q0 = pos >> 5, r = pos & 31;
-#pragma unroll
-    for (int d = 0; d < ND; d += 2) {
-        const uint32_t pair = D[d] | ((d + 1 < ND ? D[d + 1] : 0u) << 16);
-        if (!pair) continue;
-        const uint64_t w = (uint64_t)pair << r;
-        const int k0 = q0 + d / 2;
-        if (k0 < S) R[k0] += (int64_t)(w & M32);
-        if (k0 + 1 < S) R[k0 + 1] += (int64_t)(w >> 32);
-    }
-    normalise<S>(R);
+    const bool neg = normalise<S>(R);
     finish_cell<F64>(F, R, neg, flags, i, j);
 }
 
 template <bool F64, int TM, int TN>
-__global__ void __launch_bounds__(TM * TN) crt_finish_kernel(FArgs F, const LineStat *ra,
-                                                             const LineStat *cb, const CrtHdr *h,
-                                                             const uint8_t *y, uint64_t y_plane,
-                                                             int gn) {
+__global__ void __launch_bounds__(TM * TN) crt_fast_kernel(FArgs F, const LineStat *ra,
+                                                           const LineStat *cb, const CrtHdr *h,
+                                                           const uint8_t *y, uint64_t y_plane,
+                                                           int gn) {
+    const int t = threadIdx.x;
+    const uint64_t i = (uint64_t)(blockIdx.x / gn) * TM + t / TN;
+    const uint64_t j = (uint64_t)(blockIdx.x % gn) * TN + t % TN;
+    if (i >= F.m || j >= F.n) return;
+    const CrtHdr hd = *h;
+    const LineStat sa = ra[i], sb = cb[j];
+    if (!fast_cell(F, hd, sa, sb)) return;
+    const int nd = crt_nd16[hd.nmod];
+    if (nd <= 8) crt_fast_cell<F64, 8>(F, sa, sb, hd.nmod, y, y_plane, i, j);
+    else if (nd <= 12) crt_fast_cell<F64, 12>(F, sa, sb, hd.nmod, y, y_plane, i, j);
+    else if (nd <= 16) crt_fast_cell<F64, 16>(F, sa, sb, hd.nmod, y, y_plane, i, j);
+    else crt_fast_cell<F64, CRT_ND16>(F, sa, sb, hd.nmod, y, y_plane, i, j);
+}
+
+template <bool F64, int TM, int TN>
+__global__ void __launch_bounds__(TM * TN) crt_general_kernel(FArgs F, const LineStat *ra,
+                                                              const LineStat *cb, const CrtHdr *h,
+                                                              const uint8_t *y, uint64_t y_plane,
+                                                              int nm, int gn) {
     using Fm = Fmt<F64>;
     constexpr int S = Fm::DIGITS, NT = TM * TN;
     __shared__ int64_t regs[S * NT];
@@ -1013,10 +1124,11 @@ __global__ void __launch_bounds__(TM * TN) crt_finish_kernel(FArgs F, const Line
     const uint64_t i = (uint64_t)(blockIdx.x / gn) * TM + t / TN;
     const uint64_t j = (uint64_t)(blockIdx.x % gn) * TN + t % TN;
     if (i >= F.m || j >= F.n) return;
-    const Reg R{regs + t, NT};
     const CrtHdr hd = *h;
     const LineStat sa = ra[i], sb = cb[j];
-    if (hd.crt_off || ((sa.flags | sb.flags) & LS_WIDE)) {
+    if (fast_cell(F, hd, sa, sb)) return;
+    const Reg R{regs + t, NT};
+    if (hd.crt_off) {
         for (int q = 0; q < S; ++q) R[q] = 0;
         const int flags = direct_cell<F64>(F, R, i, j);
         const bool neg = normalise<S>(R);
@@ -1025,26 +1137,30 @@ __global__ void __launch_bounds__(TM * TN) crt_finish_kernel(FArgs F, const Line
     }
     const int flags = ((sa.flags | sb.flags) & LS_DIRTY) ? flags_cell<F64>(F, i, j) : 0;
     const int nd = crt_nd16[hd.nmod];
-    if (nd <= 8) crt_cell<F64, 8>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
-    else if (nd <= 12) crt_cell<F64, 12>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
-    else if (nd <= 16) crt_cell<F64, 16>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
-    else crt_cell<F64, CRT_ND16>(F, R, sa, sb, flags, hd.nmod, y, y_plane, i, j);
+    if (nd <= 8) crt_general_cell<F64, 8>(F, R, sa, sb, flags, hd, nm, y, y_plane, i, j);
+    else if (nd <= 12) crt_general_cell<F64, 12>(F, R, sa, sb, flags, hd, nm, y, y_plane, i, j);
+    else if (nd <= 16) crt_general_cell<F64, 16>(F, R, sa, sb, flags, hd, nm, y, y_plane, i, j);
+    else crt_general_cell<F64, CRT_ND16>(F, R, sa, sb, flags, hd, nm, y, y_plane, i, j);
 }
 
-// Scratch layout of the CRT route for nm planes (every piece 256-aligned).
+// Scratch layout of the CRT route for nm moduli and up to sa_max / sb_max
+// slices per line (every piece 256-aligned).
 struct CrtLayout {
     uint64_t hdr, ra, cb, ap, bp, y, total;
     uint64_t kp, np, a_plane, b_plane, y_plane;
+    int nm, sa_max, sb_max;
 };
 
 static inline uint64_t al256(uint64_t v) { return (v + 255) & ~255ull; }
 
-static CrtLayout crt_layout(uint64_t m, uint64_t k, uint64_t n, int nm) {
+static CrtLayout crt_layout(uint64_t m, uint64_t k, uint64_t n, int nm, int smax) {
     CrtLayout L;
+    L.nm = nm;
+    L.sa_max = L.sb_max = smax;
     L.kp = (k + DL_BK - 1) / DL_BK * DL_BK;
     L.np = (n + 15) / 16 * 16;
-    L.a_plane = al256(m * L.kp);
-    L.b_plane = al256(L.kp * L.np);
+    L.a_plane = al256(m * (uint64_t)smax * L.kp);
+    L.b_plane = al256((uint64_t)smax * L.kp * L.np);
     L.y_plane = al256(m * n);
     L.hdr = 0;
     L.ra = 256;
@@ -1052,14 +1168,25 @@ static CrtLayout crt_layout(uint64_t m, uint64_t k, uint64_t n, int nm) {
     L.ap = L.cb + al256(n * sizeof(LineStat));
     L.bp = L.ap + (uint64_t)nm * L.a_plane;
     L.y = L.bp + (uint64_t)nm * L.b_plane;
-    L.total = L.y + (uint64_t)nm * L.y_plane;
+    L.total = L.y + (uint64_t)(2 * smax - 1) * nm * L.y_plane;
     return L;
 }
 
+// The most slices a line of this format can need (its exponent range plus
+// the significand, in WIDE_BITS slices), within the i32 bound on a
+// diagonal's depth (slices * kp <= 2^17).
+static int crt_slice_cap(bool f64, uint64_t k) {
+    const int width = f64 ? (1024 + 1074) : (128 + 149);
+    int s = (width + WIDE_BITS - 1) / WIDE_BITS;
+    const uint64_t kp = (k + DL_BK - 1) / DL_BK * DL_BK;
+    while (s > 1 && (uint64_t)s * kp > (uint64_t)CRT_BK_MAX) --s;
+    return s;
+}
+
 template <bool F64>
-static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, int nm,
-                             hipStream_t s) {
+static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, hipStream_t s) {
     const uint64_t m = F.m, k = F.k, n = F.n;
+    const int nm = L.nm;
     CrtHdr *h = (CrtHdr *)(scratch + L.hdr);
     LineStat *ra = (LineStat *)(scratch + L.ra), *cb = (LineStat *)(scratch + L.cb);
     int8_t *ap = (int8_t *)(scratch + L.ap), *bp = (int8_t *)(scratch + L.bp);
@@ -1078,42 +1205,48 @@ static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, 
         hipLaunchKernelGGL((line_stats_kernel<F64, false>), dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
                            s, F.b, F.bcs, F.brs, n, k, cb);
     // 2. plan.
-    hipLaunchKernelGGL(crt_plan_kernel, dim3(1), dim3(256), 0, s, ra, m, cb, n, k, nm, h);
-    // 3. residue planes: A as [m][kp], B as [kp][np].
+    hipLaunchKernelGGL(crt_plan_kernel, dim3(1), dim3(256), 0, s, ra, m, cb, n, k, nm, L.sa_max,
+                       L.sb_max, h);
+    // 3. residue planes.
     {
-        const uint64_t ta = m * (L.kp / 4), tb = L.kp * (L.np / 4);
-        const auto blocks = [](uint64_t t) { return (unsigned)std::min<uint64_t>((t + 255) / 256, 2048); };
+        const uint64_t ta = (uint64_t)L.sa_max * m * (L.kp / 4), tb = (uint64_t)L.sb_max * L.kp * (L.np / 4);
+        const auto blocks = [](uint64_t t) { return (unsigned)std::min<uint64_t>((t + 255) / 256, 4096); };
         hipLaunchKernelGGL((residue_kernel<F64, true>), dim3(blocks(ta)), dim3(256), 0, s, F.a, F.ars,
-                           F.acs, m, k, m, L.kp, ra, h, ap, L.a_plane);
+                           F.acs, m, k, L.kp, L.np, L.sa_max, ra, h, ap, L.a_plane);
         hipLaunchKernelGGL((residue_kernel<F64, false>), dim3(blocks(tb)), dim3(256), 0, s, F.b, F.brs,
-                           F.bcs, k, n, L.kp, L.np, cb, h, bp, L.b_plane);
+                           F.bcs, k, n, L.kp, L.np, L.sb_max, cb, h, bp, L.b_plane);
     }
-    // 4. residue GEMMs, one grid z per modulus.
+    // 4. residue GEMMs: grid y = diagonal, z = modulus.
     {
         constexpr int BM = 256, BN = 256;
-        Opnd A{ap, (int64_t)L.kp, 1, m};
-        Opnd B{bp, 1, (int64_t)L.np, n};
-        ResOut R{y, L.y_plane, L.a_plane, L.b_plane, h};
+        ResOut R{y, L.y_plane, nm, ap, bp, L.a_plane, L.b_plane, L.kp, L.np, L.sa_max, L.sb_max, h};
         const int gm = (int)((m + BM - 1) / BM), gn = (int)((n + BN - 1) / BN);
-        const dim3 grid((unsigned)(gm * gn), 1, (unsigned)nm);
+        const dim3 grid((unsigned)(gm * gn), (unsigned)(L.sa_max + L.sb_max - 1), (unsigned)nm);
         switch (dl_variant()) {
         case DL_W4:
-            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 2, false>), grid, dim3(256), 0, s, A, B, L.kp, gm, gn, R);
+            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 2, false>), grid, dim3(256), 0, s, m, n, gm, gn, R);
             break;
-        case DL_W8PF:
-            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, true>), grid, dim3(512), 0, s, A, B, L.kp, gm, gn, R);
+        case DL_W8:
+            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, false>), grid, dim3(512), 0, s, m, n, gm, gn, R);
             break;
         default:
-            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, false>), grid, dim3(512), 0, s, A, B, L.kp, gm, gn, R);
+            hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, true>), grid, dim3(512), 0, s, m, n, gm, gn, R);
             break;
         }
     }
-    // 5. reconstruction, epilogue, encode.
+    // 5. reconstruction, epilogue, encode: the register epilogue's cells,
+    // then every other cell.
+    {
+        constexpr int TM = 4, TN = 64;
+        const uint64_t gm = (m + TM - 1) / TM, gn = (n + TN - 1) / TN;
+        hipLaunchKernelGGL((crt_fast_kernel<F64, TM, TN>), dim3((unsigned)(gm * gn)), dim3(TM * TN), 0, s, F,
+                           ra, cb, h, y, L.y_plane, (int)gn);
+    }
     {
         constexpr int TM = F64 ? 1 : 4, TN = 64;
         const uint64_t gm = (m + TM - 1) / TM, gn = (n + TN - 1) / TN;
-        hipLaunchKernelGGL((crt_finish_kernel<F64, TM, TN>), dim3((unsigned)(gm * gn)), dim3(TM * TN), 0, s,
-                           F, ra, cb, h, y, L.y_plane, (int)gn);
+        hipLaunchKernelGGL((crt_general_kernel<F64, TM, TN>), dim3((unsigned)(gm * gn)), dim3(TM * TN), 0, s,
+                           F, ra, cb, h, y, L.y_plane, nm, (int)gn);
     }
     return hipGetLastError();
 }
@@ -1124,11 +1257,11 @@ using namespace uor;
 
 extern "C" uint64_t uor_gfx950_suggested_scratch_float(int is_f64, uint64_t m, uint64_t k,
                                                        uint64_t n) {
-    // The CRT route's planes for every modulus it may use, plus alignment
-    // slack; 0 where that route does not apply (the direct route needs none).
-    (void)is_f64;
+    // The CRT route's planes for every modulus and every slice a line of
+    // this format can need, plus alignment slack; 0 where that route does
+    // not apply (the direct route needs none).
     if (m == 0 || n == 0 || k == 0 || k > (uint64_t)CRT_BK_MAX) return 0;
-    return crt_layout(m, k, n, CRT_NMAX).total + 256;
+    return crt_layout(m, k, n, CRT_NMAX, crt_slice_cap(is_f64 != 0, k)).total + 256;
 }
 
 extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_view *b,
@@ -1147,7 +1280,9 @@ extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_vi
     FArgs F{A.base, A.rs, A.cs, B.base, B.rs, B.cs, C.base, C.rs, C.cs,
             A.rows, A.cols, B.cols, alpha, beta, encode};
     hipStream_t s = (hipStream_t)stream;
-    // The CRT route when the offer holds at least one modulus' planes.
+    // The CRT route when the offer holds at least one modulus' planes: the
+    // most slices the format can need if they fit with 40 or more moduli,
+    // else fewer slices, else unsliced with what fits.
     int nm = 0;
     CrtLayout L{};
     char *sc = nullptr;
@@ -1155,25 +1290,27 @@ extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_vi
         const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
         const uint64_t have = scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
         sc = (char *)p1;
-        for (int q = CRT_NMAX; q >= 1; --q) {
-            const CrtLayout Lq = crt_layout(F.m, F.k, F.n, q);
-            if (Lq.total <= have) {
-                nm = q;
-                L = Lq;
-                break;
+        for (int sm = crt_slice_cap(is_f64 != 0, F.k); sm >= 1 && nm == 0; --sm) {
+            for (int q = CRT_NMAX; q >= (sm > 1 ? 40 : 1); --q) {
+                const CrtLayout Lq = crt_layout(F.m, F.k, F.n, q, sm);
+                if (Lq.total <= have) {
+                    nm = q;
+                    L = Lq;
+                    break;
+                }
             }
         }
         const uint64_t gm = (F.m + 255) / 256, gn = (F.n + 255) / 256;
         if (gm * gn > 0x7fffffffull || F.m > 0x7fffffffull || F.n > 0x7fffffffull) nm = 0;
     }
     if (nm > 0) {
-        UOR_HIP(is_f64 ? launch_crt<true>(F, sc, L, nm, s) : launch_crt<false>(F, sc, L, nm, s));
+        UOR_HIP(is_f64 ? launch_crt<true>(F, sc, L, s) : launch_crt<false>(F, sc, L, s));
         if (route) {
             route->kind = UOR_ROUTE_FLOAT_CRT;
             route->tile_m = route->tile_n = 256;
             route->tile_k = DL_BK;
             route->split_k = 1;
-            route->launches = 7;
+            route->launches = 8;
             route->moduli = nm;  // planes offered; the device uses the fewest that suffice
             route->scratch_used = L.total;
         }
