@@ -195,19 +195,25 @@ __device__ inline void carry_mid(const Reg &R) {
     R[S - 1] += carry;
 }
 
-// Normalise to a magnitude in [0, 2^(32S)) with digits in [0, 2^32); returns
-// true when the value is negative.  The register's headroom keeps the top
-// slot's remainder at 0 or -1.
+// Normalise to a magnitude with digits in [0, 2^32); returns true when the
+// value is negative.  Only slots [lo, hi] may be nonzero (the others stay
+// zero); slot hi's headroom keeps its remainder at 0 or -1.
 template <int S>
-__device__ inline bool normalise(const Reg &R) {
-    carry_mid<S>(R);
-    const int64_t top = R[S - 1];
+__device__ inline bool normalise(const Reg &R, int lo = 0, int hi = S - 1) {
+    int64_t carry = 0;
+    for (int q = lo; q < hi; ++q) {
+        const int64_t v = R[q] + carry;
+        R[q] = v & M32;
+        carry = v >> 32;  // arithmetic shift: floor division
+    }
+    const int64_t top = R[hi] + carry;
     const bool neg = top < 0;
-    R[S - 1] = top & M32;
+    R[hi] = top & M32;
     if (neg) {
-        // Two's complement over S digits: invert and add one.
+        // Two's complement over [lo, hi] (the zero digits below lo pass the
+        // +1 through unchanged): invert and add one.
         uint64_t c = 1;
-        for (int q = 0; q < S; ++q) {
+        for (int q = lo; q <= hi; ++q) {
             const uint64_t v = (uint64_t)(~R[q] & M32) + c;
             R[q] = (int64_t)(v & M32);
             c = v >> 32;
@@ -216,10 +222,12 @@ __device__ inline bool normalise(const Reg &R) {
     return neg;
 }
 
+// R *= f over slots [lo, hi]; the caller leaves 64 bits of headroom above
+// the value inside the window.
 template <int S>
-__device__ inline void mul_small(const Reg &R, uint64_t f) {
+__device__ inline void mul_small(const Reg &R, uint64_t f, int lo = 0, int hi = S - 1) {
     uint64_t carry = 0;  // below 2^64: digit * f + carry < 2^96
-    for (int q = 0; q < S; ++q) {
+    for (int q = lo; q <= hi; ++q) {
         const u128 t = (u128)(uint64_t)R[q] * f + carry;
         R[q] = (int64_t)((uint64_t)t & M32);
         carry = (uint64_t)(t >> 32);
@@ -279,7 +287,8 @@ __device__ inline int reg_bit(const Reg &R, int S, int i) {
 // impl_encode_into_float (acc.rs:1734-1868) from a magnitude register whose
 // bit 0 has exponent RB.
 template <bool F64, int S>
-__device__ inline uint64_t encode_reg(const Reg &R, bool neg, int flags, int mode) {
+__device__ inline uint64_t encode_reg(const Reg &R, bool neg, int flags, int mode, int lo = 0,
+                                      int hi = S - 1) {
     using F = Fmt<F64>;
     constexpr int MANT = F::MANT, EXPO = F::EXPO, P = MANT + 1;
     constexpr uint64_t EXPMASK = (1ull << EXPO) - 1;
@@ -289,7 +298,7 @@ __device__ inline uint64_t encode_reg(const Reg &R, bool neg, int flags, int mod
         return (s << (MANT + EXPO)) | (EXPMASK << MANT);
     }
     int top = -1;
-    for (int q = S - 1; q >= 0; --q) {
+    for (int q = hi; q >= lo; --q) {
         const uint32_t d = (uint32_t)R[q];
         if (d) {
             top = 32 * q + 31 - __builtin_clz(d);
@@ -310,7 +319,7 @@ __device__ inline uint64_t encode_reg(const Reg &R, bool neg, int flags, int mod
         round_bit = reg_bit(R, S, lsb - 1);
         const int below = lsb - 1;  // bits [0, below) feed the sticky bit
         const int qb = below >> 5;
-        for (int t = 0; t < qb && t < S; ++t)
+        for (int t = lo; t < qb && t < S; ++t)
             if ((uint32_t)R[t]) sticky = 1;
         if (!sticky && qb < S && (below & 31)) {
             const uint32_t msk = (1u << (below & 31)) - 1;
@@ -365,18 +374,20 @@ __device__ inline void store_bits(char *base, int64_t idx, uint64_t v) {
 
 // The epilogue of one cell from its normalised register: alpha, beta * C,
 // encode, store.  `neg` is the sign of the register's value.
+// Slots outside [lo, hi] are zero and stay so until beta * C is added
+// (which then widens the window to the whole register).
 template <bool F64>
 __device__ inline void finish_cell(const FArgs &F, const Reg &R, bool neg, int flags, uint64_t i,
-                                   uint64_t j) {
+                                   uint64_t j, int lo = 0, int hi = Fmt<F64>::DIGITS - 1) {
     using Fm = Fmt<F64>;
     constexpr int S = Fm::DIGITS;
     flags = scale_flags(flags, F.alpha);
     if (F.alpha == 0) {
-        for (int q = 0; q < S; ++q) R[q] = 0;
+        for (int q = lo; q <= hi; ++q) R[q] = 0;
         neg = false;
     } else if (F.alpha != 1) {
         const uint64_t fa = F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha;
-        mul_small<S>(R, fa);
+        mul_small<S>(R, fa, lo, hi);
         if (F.alpha < 0) neg = !neg;
     }
     const int64_t ci = (int64_t)i * F.crs + (int64_t)j * F.ccs;
@@ -391,8 +402,10 @@ __device__ inline void finish_cell(const FArgs &F, const Reg &R, bool neg, int f
             add_signed<S>(R, &neg, (u128)d.mant * fb, d.exp - Fm::RB, (d.neg != 0) != (F.beta < 0));
         }
         flags |= scale_flags(g, F.beta);
+        lo = 0;
+        hi = S - 1;
     }
-    store_bits<F64>(F.c, ci, encode_reg<F64, S>(R, neg, flags, F.mode));
+    store_bits<F64>(F.c, ci, encode_reg<F64, S>(R, neg, flags, F.mode, lo, hi));
 }
 
 // ------------------------------------------------------- direct route --
@@ -1069,6 +1082,9 @@ __device__ inline void crt_general_cell(const FArgs &F, const Reg &R, const Line
     using Fm = Fmt<F64>;
     constexpr int S = Fm::DIGITS;
     for (int q = 0; q < S; ++q) R[q] = 0;
+    // The slots the diagonals touch, plus headroom for their carries, the
+    // sign and an alpha of up to 64 bits.
+    int wlo = S - 1, whi = 0;
     if (hd.nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY)) {
         const int ndiag = hd.sa + hd.sb - 1;
         const int E = sa.lo + sb.lo;
@@ -1077,6 +1093,8 @@ __device__ inline void crt_general_cell(const FArgs &F, const Reg &R, const Line
             const bool neg = crt16<ND>(y + (uint64_t)dg * nm * y_plane, y_plane, i * F.n + j, hd.nmod, X);
             const int pos = E - Fm::RB + hd.w * dg;
             const int q0 = pos >> 5, r = pos & 31;
+            wlo = min(wlo, q0);
+            whi = max(whi, q0 + (ND + 1) / 2);
 #pragma unroll
             for (int dd = 0; dd < ND; dd += 2) {
                 const uint32_t pair = X[dd] | ((dd + 1 < ND ? X[dd + 1] : 0u) << 16);
@@ -1089,8 +1107,10 @@ __device__ inline void crt_general_cell(const FArgs &F, const Reg &R, const Line
             }
         }
     }
-    const bool neg = normalise<S>(R);
-    finish_cell<F64>(F, R, neg, flags, i, j);
+    if (wlo > whi) wlo = whi = 0;
+    whi = min(S - 1, whi + 4);
+    const bool neg = normalise<S>(R, wlo, whi);
+    finish_cell<F64>(F, R, neg, flags, i, j, wlo, whi);
 }
 
 template <bool F64, int TM, int TN>
