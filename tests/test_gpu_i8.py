@@ -312,3 +312,29 @@ def test_fused_tile_epilogues(uor, dev, case):
     # padding columns untouched
     assert np.array_equal(got[:, n:], c0[off:off + m * ldc].reshape(m, ldc)[:, n:])
     assert bits in (16, 32, 64)
+
+
+@pytest.mark.parametrize("m,n,k", [(4096 + 36, 4096 + 48, 64), (4096, 4096 + 16, 192),
+                                   (4300, 4112, 320), (4096, 4096, 896), (4352, 4096, 8192 + 64)])
+def test_tile256_ragged_edges_and_depths(uor, dev, m, n, k):
+    """The 256x256 direct-to-LDS tile at ragged m and n (partial edge tiles,
+    rows and columns past the edge computed and discarded) and depths of 1, 3,
+    5, 14 and 129 steps of 64 (each remainder of the four-stage loop), with
+    alpha = 3, beta = -1.  Expected values from an exact float64 product
+    (|sum| <= k * 2^14 < 2^53)."""
+    lda, ldb, ldc = k + 16, n + 16, n + 8
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    a = torch.from_numpy(rng.integers(-128, 128, m * lda).astype(np.int8)).to(dev)
+    b = torch.from_numpy(rng.integers(-128, 128, k * ldb).astype(np.int8)).to(dev)
+    c0 = rng.integers(-(1 << 20), 1 << 20, m * ldc).astype(np.int32)
+    c = torch.from_numpy(c0.copy()).to(dev)
+    st, route = uor.gemm_i8(a, (m, k), (lda, 1), b, (k, n), (ldb, 1), c, (m, n), (ldc, 1), out="i32",
+                            alpha=3, beta=-1)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == 256, route
+    S = (a.view(m, lda)[:, :k].double() @ b.view(k, ldb)[:, :n].double()).cpu().numpy().astype(np.int64)
+    C0 = c0.reshape(m, ldc).astype(np.int64)
+    want = 3 * S - C0[:, :n]
+    got = c.cpu().numpy().reshape(m, ldc)
+    assert np.array_equal(got[:, :n].astype(np.int64), want)
+    assert np.array_equal(got[:, n:], c0.reshape(m, ldc)[:, n:])

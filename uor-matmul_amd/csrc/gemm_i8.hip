@@ -645,6 +645,186 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
     }
 }
 
+// The 256x256 tile on four scheduled waves (s4_loop), persistent: one
+// workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...  Each
+// wave's 128x128 block is 4x4 accumulators of 32x32.  The next tile's first
+// three stages are requested before this tile's epilogue, so their loads
+// overlap its C traffic.
+
+// The epilogue straight from the accumulators: lane (l32, half) of block
+// (i, j) holds column 32j + l32 of rows 8(r>>2) + 4half + (r&3), r < 16, so
+// one instruction per r moves two rows of 32 consecutive columns.
+//
+// A wave whose 128x128 block lies inside C (with non-negative strides and
+// offsets below 2^31 bytes) goes through a buffer resource based at the
+// block's corner: each access is the lane's 32-bit offset plus a uniform
+// scalar offset, so addresses cost no vector registers.  The priors of block
+// row i+1 are requested before block row i is combined and stored (fenced, so
+// at most two block rows of priors are live), and their waits are partial.
+// Any other block takes the per-cell checked path.
+// C is touched once per call, so its loads and stores carry the
+// non-temporal hint (cache policy bit 1, "nt" on gfx950): measured 5% faster
+// at 8192^3 than the default policy.
+constexpr int C_NT = 2;
+template <int OB>
+__device__ inline int64_t buf_load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    if constexpr (OB == 1) return (int8_t)__builtin_amdgcn_raw_buffer_load_b8(r, vo, so, C_NT);
+    else if constexpr (OB == 2) return (int16_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, C_NT);
+    else if constexpr (OB == 4) return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, C_NT);
+    else {
+        const v2i v = (v2i)__builtin_amdgcn_raw_buffer_load_b64(r, vo, so, C_NT);
+        return (int64_t)(((uint64_t)(uint32_t)v[1] << 32) | (uint32_t)v[0]);
+    }
+}
+template <int OB>
+__device__ inline void buf_store(__amdgpu_buffer_rsrc_t r, int vo, int so, int64_t x) {
+    if constexpr (OB == 1) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)x, r, vo, so, C_NT);
+    else if constexpr (OB == 2) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)x, r, vo, so, C_NT);
+    else if constexpr (OB == 4) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)x, r, vo, so, C_NT);
+    else {
+        typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(v2u{(unsigned)(uint64_t)x, (unsigned)((uint64_t)x >> 32)}, r, vo, so,
+                                              C_NT);
+    }
+}
+
+template <int OB, bool RD>
+__device__ inline void s4_epilogue_full(const OutArgs &out, const v16i (&acc)[4][4], char *corner, int vo,
+                                        int srs, int scs) {
+    typedef typename std::conditional<OB == 8, int64_t, int32_t>::type P;
+    constexpr int NB = OB == 8 ? 1 : 2;  // prior batches in flight
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(corner, 0, 0x7FFFFFFF, 0x00020000);
+    auto offs = [&](int i, int j, int r) -> int {
+        return (32 * i + 8 * (r >> 2) + (r & 3)) * srs + (32 * j) * scs;
+    };
+    P pr[NB][4][16];
+    auto load = [&](int i, P (&p)[4][16]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[j][r] = (P)buf_load<OB>(rs, vo, offs(i, j, r));
+    };
+    if constexpr (RD && NB == 2) load(0, pr[0]);
+    S4_FENCE();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (RD) {
+            if constexpr (NB == 2) {
+                if (i + 1 < 4) load(i + 1, pr[(i + 1) & 1]);
+            } else {
+                load(i, pr[0]);
+            }
+        }
+        S4_FENCE();
+        const P (&p)[4][16] = pr[NB == 2 ? (i & 1) : 0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int64_t x = (int64_t)acc[i][j][r] * out.alpha;
+                if constexpr (RD) x += (int64_t)p[j][r] * out.beta;
+                buf_store<OB>(rs, vo, offs(i, j, r), (int64_t)encode_int((i128)x, OB, out.mode));
+            }
+        S4_FENCE();
+    }
+}
+
+template <int OB>
+__device__ inline void s4_epilogue_fast(const OutArgs &out, const v16i (&acc)[4][4], uint64_t rw, uint64_t cw,
+                                        uint64_t M, uint64_t N) {
+    const int lane = threadIdx.x & 63, half = lane >> 5, l32 = lane & 31;
+    const bool inside = rw + 128 <= M && cw + 128 <= N;
+    const bool small = out.rs >= 0 && out.cs >= 0 && (127 * out.rs + 127 * out.cs + 1) * OB < ((int64_t)1 << 31);
+    if (inside && small) {
+        const int srs = (int)(out.rs * OB), scs = (int)(out.cs * OB);
+        char *const corner = out.base + ((int64_t)rw * out.rs + (int64_t)cw * out.cs) * OB;
+        const int vo = 4 * half * srs + l32 * scs;
+        if (out.beta != 0) s4_epilogue_full<OB, true>(out, acc, corner, vo, srs, scs);
+        else s4_epilogue_full<OB, false>(out, acc, corner, vo, srs, scs);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint64_t row = rw + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3), col = cw + 32 * j + l32;
+                if (row < M && col < N)
+                    linear_finish<OB, true>(out.base + ((int64_t)row * out.rs + (int64_t)col * out.cs) * OB,
+                                            acc[i][j][r], out.alpha, out.beta, out.mode);
+            }
+}
+
+template <bool FAST, int OB>
+__global__ void __launch_bounds__(256, 1)
+gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
+    using L = S4::L;
+    constexpr bool DIRECT = FAST && OB <= 8;
+    __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
+    const int ntiles = gm * gn;
+    int tile = blockIdx.x;
+    if (tile >= ntiles) return;
+    const int nk = (int)(K / DL_BK);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    S4Lane ln;
+    S4Scalars sc;
+    s4_setup_lane(B, lds, ln, sc);
+    int tm, tn;
+    tile_coords(tile, gm, gn, &tm, &tn);
+    s4_setup_tile(A, B, (uint64_t)tm * 256, (uint64_t)tn * 256, 0, ln, sc);
+    s4_prologue(ln, sc, nk);
+    for (;;) {
+        v16i acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
+        s4_loop(ln, sc, nk, acc);
+        stage_barrier();  // every wave's stage reads retired: the slots are free
+        const uint64_t rw = (uint64_t)tm * 256 + wm * 128, cw = (uint64_t)tn * 256 + wn * 128;
+        const int next = tile + (int)gridDim.x;
+        int nm = 0, nn = 0;
+        if (next < ntiles) tile_coords(next, gm, gn, &nm, &nn);
+        if constexpr (DIRECT) {
+            if (next < ntiles) {
+                s4_setup_tile(A, B, (uint64_t)nm * 256, (uint64_t)nn * 256, 0, ln, sc);
+                s4_prologue(ln, sc, nk);
+            }
+            s4_epilogue_fast<OB>(out, acc, rw, cw, A.mn, B.mn);
+        } else {
+            // The full i128 evaluation: one 32x32 block at a time through a
+            // padded park, then the next tile's stages.
+            int *park = (int *)lds + wave * (32 * 33);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        park[(8 * (r >> 2) + 4 * half + (r & 3)) * 33 + l32] = acc[i][j][r];
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                    __builtin_amdgcn_wave_barrier();
+                    encode_block<OB, FAST>(out, park, rw + 32 * i, cw + 32 * j + l32, A.mn, B.mn);
+                    __builtin_amdgcn_wave_barrier();
+                }
+            }
+            __syncthreads();
+            if (next < ntiles) {
+                s4_setup_tile(A, B, (uint64_t)nm * 256, (uint64_t)nn * 256, 0, ln, sc);
+                s4_prologue(ln, sc, nk);
+            }
+        }
+        if (next >= ntiles) break;
+        tile = next;
+        tm = nm;
+        tn = nn;
+    }
+}
+
 // The encode step over an exact partial-sum workspace (or over a zero sum
 // when k == 0: C := enc(beta * C)).
 template <bool FAST, bool ZERO>
@@ -700,6 +880,43 @@ static hipError_t launch_dl(const Opnd &A, const Opnd &B, const OutArgs &out, ui
     dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
     hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), 0, s, A, B, out, K, kslice, gm, gn);
     return hipGetLastError();
+}
+
+static int device_cus() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        return n;
+    }();
+    return cus;
+}
+
+template <bool FAST>
+static hipError_t launch_s4(const Opnd &A, const Opnd &B, const OutArgs &out, uint64_t K, hipStream_t s) {
+    auto kern = gemm_i8_s4_kernel<FAST, 4>;
+    switch (out.ob) {
+    case 1: kern = gemm_i8_s4_kernel<FAST, 1>; break;
+    case 2: kern = gemm_i8_s4_kernel<FAST, 2>; break;
+    case 8: kern = gemm_i8_s4_kernel<FAST, 8>; break;
+    case 16: kern = gemm_i8_s4_kernel<false, 16>; break;
+    default: break;
+    }
+    const int gm = (int)((A.mn + 255) / 256), gn = (int)((B.mn + 255) / 256);
+    const int tiles = gm * gn;
+    const int grid = tiles < device_cus() ? tiles : device_cus();
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, s, A, B, out, K, gm, gn);
+    return hipGetLastError();
+}
+
+// The scheduled four-wave loop addresses its operands as a 64-bit scalar base
+// plus 32-bit per-lane offsets: every row of A and 64 k-rows of B must lie
+// within 4 GiB of the operand's base, with positive strides.
+static bool s4_ok(const Opnd &A, const Opnd &B) {
+    if (A.s_mn <= 0 || B.s_k <= 0) return false;
+    const unsigned __int128 a_span = (unsigned __int128)A.mn * (uint64_t)A.s_mn + 64;
+    const unsigned __int128 b_span = (unsigned __int128)64 * (uint64_t)B.s_k + B.mn + 16;
+    return a_span < ((unsigned __int128)1 << 32) && b_span < ((unsigned __int128)1 << 32);
 }
 
 // The direct-to-LDS pipeline applies when both operands stream in 16-byte
@@ -863,7 +1080,10 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
     int bm;
     if (t256 >= 256 && dl_ok(pair, K, N)) {
         bm = 256;
-        switch (dl_variant()) {
+        const int v = dl_variant();
+        if (v == DL_S4 && s4_ok(A, B)) {
+            UOR_HIP((launch_s4<FAST>(A, B, out, K, s)));
+        } else switch (v == DL_S4 ? (int)DL_W8PF : v) {
         case DL_W4: UOR_HIP((launch_dl<256, 256, 2, 2, EPI_FUSED, FAST, false>(A, B, out, K, 0, 1, s))); break;
         case DL_W8PF: UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST, true>(A, B, out, K, 0, 1, s))); break;
         default: UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST, false>(A, B, out, K, 0, 1, s))); break;

@@ -10,17 +10,19 @@
 
 namespace uor {
 
-// Which 256x256 pipeline runs (UOR_GFX950_DL_VARIANT at load time): 8 waves
-// (two per SIMD) with the first half of each step's fragments prefetched one
-// step ahead (w8pf, the default), the same without the prefetch (w8), or 4
-// waves (one per SIMD, w4).  All give the same bytes.
-enum : int { DL_W8 = 0, DL_W4 = 1, DL_W8PF = 2 };
+// Which 256x256 pipeline runs (UOR_GFX950_DL_VARIANT at load time): 4 waves
+// (one per SIMD) with the explicitly interleaved schedule (s4, the default),
+// 8 waves (two per SIMD) with the first half of each step's fragments
+// prefetched one step ahead (w8pf), the same without the prefetch (w8), or 4
+// waves in compiler order (w4).  All give the same bytes.
+enum : int { DL_W8 = 0, DL_W4 = 1, DL_W8PF = 2, DL_S4 = 3 };
 static inline int dl_variant() {
     static int v = [] {
         const char *e = getenv("UOR_GFX950_DL_VARIANT");
         if (e && !strcmp(e, "w8")) return (int)DL_W8;
         if (e && !strcmp(e, "w4")) return (int)DL_W4;
-        return (int)DL_W8PF;
+        if (e && !strcmp(e, "w8pf")) return (int)DL_W8PF;
+        return (int)DL_S4;
     }();
     return v;
 }
@@ -39,10 +41,11 @@ struct Opnd {
 // Tile index -> (tile row, tile column).  Workgroups are dealt round-robin to
 // the 8 XCDs, so consecutive ids are remapped onto one XCD first, then walked
 // in groups of 8 tile rows so that the tiles one XCD holds at a time share
-// A rows and B columns in its L2.
-__device__ inline void tile_of(int gm, int gn, int *tm, int *tn) {
+// A rows and B columns in its L2.  (A persistent grid whose size is a
+// multiple of 8 keeps tile id b on XCD b % 8 as well.)
+__device__ inline void tile_coords(int id, int gm, int gn, int *tm, int *tn) {
     int nb = gm * gn;
-    int b = blockIdx.x;
+    int b = id;
     if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
     const int G = 8;
     int per = G * gn;
@@ -53,6 +56,7 @@ __device__ inline void tile_of(int gm, int gn, int *tm, int *tn) {
     *tm = first + w % gs;
     *tn = w / gs;
 }
+__device__ inline void tile_of(int gm, int gn, int *tm, int *tn) { tile_coords(blockIdx.x, gm, gn, tm, tn); }
 
 // ------------------------------------------------- direct-to-LDS pipeline --
 //
@@ -347,6 +351,232 @@ __device__ inline void dl_mainloop_pf(const Opnd &A, const Opnd &B, uint64_t m0,
     }
 #undef UOR_DL_PF_STEP
     wait_vm<0>();
+}
+
+// ------------------------------------------ four-wave scheduled pipeline --
+//
+// The 256x256 tile with four waves (2x2, one per SIMD), each owning a 128x128
+// block of the tile (4x4 accumulators of 32x32): per 64-deep step a wave issues
+// 32 MFMAs against 8 ds_read_b128 (A) and 16 ds_read_b64_tr_b8 (B), a third
+// less LDS traffic per MFMA than the eight-wave 128x64 split.  With one wave
+// per SIMD nothing overlaps unless the wave itself interleaves, so every step
+// is written out in issue order and fenced (sched_barrier) against the
+// scheduler, one memory instruction after each MFMA:
+//
+//   P1  the 16 MFMAs of k-half 0 (fragments f0, read during the previous
+//       step); after MFMA q < 12 the q-th read of k-half 1 (f1), after MFMAs
+//       12..15 the four A loads of stage t+3 (into stage t-1's slot).
+//   P2  wait until this wave's loads of stage t+1 have landed and its f1 reads
+//       have returned, then the workgroup barrier.  After it stage t+1 is
+//       complete for every wave, and every read of slot t has retired, so the
+//       next step may refill that slot (with stage t+4).
+//   P3  the 16 MFMAs of k-half 1, each of the first 12 followed by one read of
+//       step t+1's f0, the last four by the four B loads of stage t+3.
+//
+// A stage's loads are issued about three steps before its first read.  The
+// loads use the scalar-base form (global_load_lds_dwordx4 voffset, sbase):
+// per-lane 32-bit offsets fixed for the whole k loop and one 64-bit scalar
+// base per operand advanced per step, so the host routes here only views
+// whose offsets fit in 32 bits.
+
+struct S4 {
+    static constexpr int BM = 256, BN = 256, NT = 256;
+    using L = DlLayout<256, 256>;
+    static constexpr int LOADS = 8;  // LDS-DMA loads per thread per stage (4 A, 4 B)
+};
+
+// Per-lane constants of the scheduled loop.
+struct S4Lane {
+    uint32_t voa[4], vob[4];  // global offsets of this lane's A / B chunks (per tile)
+    uint32_t ra[2];           // LDS byte address of A fragment 0, k-halves 0 / 1 (stage 0)
+    uint32_t rb[4];           // LDS byte address of B fragment j, k-half 0 (stage 0)
+};
+
+// Scalar state: operand bases at the next stage to load and the LDS targets.
+struct S4Scalars {
+    const int8_t *a;   // A.base + (next k0)
+    const int8_t *b;   // B.base + (next k0) * s_k
+    int64_t bstep;     // 64 * s_k
+    uint32_t mla, mlb; // LDS byte address of this wave's first A / B chunk in stage 0
+};
+
+// The tile-independent part: fragment read addresses and LDS targets.
+__device__ inline void s4_setup_lane(const Opnd &B, const char *lds, S4Lane &ln, S4Scalars &sc) {
+    using L = S4::L;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31, grp = lane >> 4, t16 = lane & 15;
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char *)lds;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+        ln.ra[ks] = base + L::a_off(wm * 128 + l32, 2 * ks + half);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int nb = wn * 128 + 32 * j + 16 * (grp & 1) + 8 * (t16 & 1);
+        const int k = 16 * (grp >> 1) + (t16 >> 1);
+        ln.rb[j] = base + L::B_OFF + L::b_off(k, nb >> 4) + (nb & 8);
+    }
+    sc.bstep = (int64_t)DL_BK * B.s_k;
+    sc.mla = base + wave * 4 * 1024;
+    sc.mlb = base + L::B_OFF + wave * 4 * 1024;
+}
+
+// The per-tile part: this lane's chunk offsets and the bases at k = kbeg.
+__device__ inline void s4_setup_tile(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t kbeg,
+                                     S4Lane &ln, S4Scalars &sc) {
+    using L = S4::L;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // A chunk: slot (wave*4 + i)*64 + lane = row*4 + physical chunk.
+        const int slot = (wave * 4 + i) * 64 + lane;
+        const int row = slot >> 2, pc = slot & 3;
+        const int c = pc ^ ((row >> 2) & 3);
+        uint64_t gr = m0 + row;
+        if (gr >= A.mn) gr = A.mn - 1;  // rows past m are computed and discarded
+        ln.voa[i] = (uint32_t)(gr * (uint64_t)A.s_mn + 16 * c);
+        // B chunk: slot = k*16 + physical chunk.
+        const int k = slot >> 4, px = slot & 15;
+        const int x = px ^ L::b_swz(k);
+        uint64_t gn = n0 + 16 * x;
+        if (gn >= B.mn) gn = 0;  // columns past n are computed and discarded
+        ln.vob[i] = (uint32_t)((uint64_t)k * (uint64_t)B.s_k + gn);
+    }
+    sc.a = A.base + kbeg;
+    sc.b = B.base + (int64_t)kbeg * B.s_k;
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// One 16-byte LDS-DMA load: lane L's bytes at sbase + voff land at m0 + 16*L.
+__device__ inline void s4_dma(uint32_t m0v, uint32_t voff, const int8_t *sbase) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0v), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Load number q (0..7: A chunks 0..3, then B chunks 0..3) of the stage in slot SLOT.
+template <int SLOT>
+__device__ inline void s4_load(const S4Lane &ln, const S4Scalars &sc, int q) {
+    using L = S4::L;
+    if (q < 4) s4_dma(sc.mla + SLOT * L::A_BYTES + q * 1024, ln.voa[q], sc.a);
+    else s4_dma(sc.mlb + SLOT * L::B_BYTES + (q - 4) * 1024, ln.vob[q - 4], sc.b);
+}
+
+// Fragment read number q (0..11) of k-half KS from slot SLOT, in the order
+// A0, B0 lo, B0 hi, A1, B1 lo, B1 hi, ...
+template <int SLOT, int KS>
+__device__ inline void s4_read(const S4Lane &ln, int q, v4i (&fa)[4], v4i (&fb)[4]) {
+    using L = S4::L;
+    typedef __attribute__((address_space(3))) const v4i lds_v4i_c;
+    const int f = q / 3, part = q % 3;
+    if (part == 0) {
+        fa[f] = *(lds_v4i_c *)(uintptr_t)(ln.ra[KS] + SLOT * L::A_BYTES + f * 32 * 64);
+    } else {
+        const v2i h = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i *)(uintptr_t)(ln.rb[f] + SLOT * L::B_BYTES + KS * 32 * 256 + (part - 1) * 8 * 256));
+        if (part == 1) { fb[f][0] = h[0]; fb[f][1] = h[1]; }
+        else { fb[f][2] = h[0]; fb[f][3] = h[1]; }
+    }
+}
+
+// The MFMA order within a half: fragment pairs in the order their reads
+// arrive (A0 B0, A1, B1, A2, B2, A3, B3).
+__device__ constexpr int s4_qi(int q) {
+    constexpr int I[16] = {0, 1, 0, 1, 2, 2, 0, 1, 2, 3, 3, 3, 0, 1, 2, 3};
+    return I[q];
+}
+__device__ constexpr int s4_qj(int q) {
+    constexpr int J[16] = {0, 0, 1, 1, 0, 1, 2, 2, 2, 0, 1, 2, 3, 3, 3, 3};
+    return J[q];
+}
+
+#define S4_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// One 64-deep step on slot CUR: the loads of stage t+3 go into slot
+// (CUR+3)%4, and P3 reads step t+1's f0 from slot (CUR+1)%4.  Every step has
+// the same shape: past the last stage the loads repeat the last stage's k
+// (their slot is never read again) and the last step's f0 reads are
+// discarded, so the vmcnt and lgkmcnt accounting is the same in every step.
+template <int CUR>
+__device__ inline void s4_step(const S4Lane &ln, S4Scalars &sc, bool advance, v4i (&fa0)[4], v4i (&fb0)[4],
+                               v4i (&fa1)[4], v4i (&fb1)[4], v16i (&acc)[4][4]) {
+    constexpr int NXT = (CUR + 1) & 3, FREE = (CUR + 3) & 3;
+    // P1
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        acc[s4_qi(q)][s4_qj(q)] =
+            __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[s4_qi(q)], fb0[s4_qj(q)], acc[s4_qi(q)][s4_qj(q)], 0, 0, 0);
+        if (q < 12) s4_read<CUR, 1>(ln, q, fa1, fb1);
+        else s4_load<FREE>(ln, sc, q - 12);
+        S4_FENCE();
+    }
+    // P2: stage t+1 landed (allowed in flight: stage t+2's eight loads and
+    // the four A loads of stage t+3 just issued), f1 returned and slot CUR's
+    // reads retired; then the barrier.
+    wait_vm<S4::LOADS + 4>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    stage_barrier();
+    S4_FENCE();
+    // P3
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        acc[s4_qi(q)][s4_qj(q)] =
+            __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[s4_qi(q)], fb1[s4_qj(q)], acc[s4_qi(q)][s4_qj(q)], 0, 0, 0);
+        if (q < 12) s4_read<NXT, 0>(ln, q, fa0, fb0);
+        else s4_load<FREE>(ln, sc, q - 8);
+        S4_FENCE();
+    }
+    if (advance) {
+        sc.a += DL_BK;
+        sc.b += sc.bstep;
+    }
+}
+
+// Stages 0..2 of a tile into slots 0..2 (a stage past the last repeats it).
+// The slots must be free: every earlier read retired and a barrier passed.
+__device__ inline void s4_prologue(const S4Lane &ln, S4Scalars &sc, int nk) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s4_load<0>(ln, sc, q);
+    if (1 < nk) sc.a += DL_BK, sc.b += sc.bstep;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s4_load<1>(ln, sc, q);
+    if (2 < nk) sc.a += DL_BK, sc.b += sc.bstep;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s4_load<2>(ln, sc, q);
+    if (3 < nk) sc.a += DL_BK, sc.b += sc.bstep;
+}
+
+// The k loop over nk >= 1 steps whose stages 0..2 the prologue issued (any
+// vector memory instructions issued after the prologue must have retired, as
+// must the prologue's stage 0 by the wait below).  Adds into acc, this
+// wave's 128x128 block.  Ends with every load landed and every LDS read of
+// this wave retired, but without a barrier.
+__device__ inline void s4_loop(const S4Lane &ln, S4Scalars &sc, int nk, v16i (&acc)[4][4]) {
+    v4i fa0[4], fb0[4], fa1[4], fb1[4];
+    wait_vm<2 * S4::LOADS>();
+    stage_barrier();
+    S4_FENCE();
+#pragma unroll
+    for (int q = 0; q < 12; ++q) s4_read<0, 0>(ln, q, fa0, fb0);
+    S4_FENCE();
+    // Step t issues stage t+3 and advances the bases while stage t+4 exists.
+    int t = 0;
+    for (; t + 4 <= nk; t += 4) {
+        s4_step<0>(ln, sc, t + 4 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<1>(ln, sc, t + 5 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<2>(ln, sc, t + 6 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<3>(ln, sc, t + 7 < nk, fa0, fb0, fa1, fb1, acc);
+    }
+    if (t < nk) s4_step<0>(ln, sc, t + 4 < nk, fa0, fb0, fa1, fb1, acc);
+    if (t + 1 < nk) s4_step<1>(ln, sc, t + 5 < nk, fa0, fb0, fa1, fb1, acc);
+    if (t + 2 < nk) s4_step<2>(ln, sc, t + 6 < nk, fa0, fb0, fa1, fb1, acc);
+    wait_vm<0>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the discarded f0 reads
 }
 
 }  // namespace uor
