@@ -207,6 +207,13 @@ def bench_deep(args, torch, uor):
     return out
 
 
+def lut_kernel_name(route):
+    """The LUT kernel a route record names (uor_gfx950_gemm_lut4's choices)."""
+    if route.get("kind") == "lut4_dot4":
+        return "lut4_dot4_pf_kernel"
+    return {1: "lut4_lds_kernel", 4: "lut4_mfma16_kernel"}.get(route.get("split_k"), "lut4_mfma_kernel")
+
+
 def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
     """the 4-bit LUT decode GEMM, m in {1, 8, 32}, k = 8192,
     n = 28672, one codebook per 128 coded rows.  Three distinct code buffers
@@ -250,7 +257,7 @@ def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
                     "GB_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                     "TOPS": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
                     "algorithmic_bytes": nbytes,
-                    "kernel": "lut4_dot4_kernel" if m <= 4 else "lut4_mfma_kernel"})
+                    "kernel": lut_kernel_name(route)})
     return out
 
 

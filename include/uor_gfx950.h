@@ -83,7 +83,8 @@ typedef struct uor_view {
 #define UOR_ROUTE_MFMA_TILE 2     /* int8 MFMA tile, fused epilogue */
 #define UOR_ROUTE_MFMA_SPLITK 3   /* int8 MFMA split-K, exact i64 partials */
 #define UOR_ROUTE_MFMA_WIDE 4     /* int8 MFMA, i64 register widening */
-#define UOR_ROUTE_LUT4_DOT4 10    /* 4-bit table-lookup, LDS codebook */
+#define UOR_ROUTE_LUT4_DOT4 10    /* 4-bit table-lookup, v_perm decode, dot4 (small m) */
+#define UOR_ROUTE_LUT4_MFMA 11    /* 4-bit table-lookup, v_perm decode into int8 MFMA */
 #define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
 #define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
 #define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */

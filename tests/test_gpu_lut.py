@@ -107,3 +107,44 @@ def test_config3_decode_shape(uor, dev, m):
     W = decode_torch(codes, n, k, books, group).to(torch.float64)
     want = a.view(m, k).to(torch.float64) @ W.T
     assert torch.equal(c.view(m, n).to(torch.float64), want), route
+    if m > 4:
+        assert route["kind"] == "lut4_mfma" and route["tile_n"] == 16, route
+
+
+@pytest.mark.parametrize("k", [1 << 18, (1 << 18) + 128])
+def test_mfma16_quarters_at_depth_limit(uor, dev, k):
+    """The 16-column MFMA tiles split k in four quarters of at most 65536
+    weights, each exact in i32 (2^16 * 2^14 = 2^30); at k = 2^18 every quarter
+    is at that limit, and one step more takes the other kernel.  All -128
+    against a codebook of -128: every cell is k * 2^14 (past i32 in total)."""
+    m, n = 8, 40
+    a = torch.full((m * k,), -128, dtype=torch.int8, device=dev)
+    codes = torch.zeros(n * k // 2, dtype=torch.uint8, device=dev)
+    books = torch.full((16 * 3,), -128, dtype=torch.int8, device=dev)
+    c = torch.zeros(m * n, dtype=torch.int64, device=dev)
+    st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, 16, c, (n, 1), out="i64")
+    torch.cuda.synchronize()
+    assert st == 0 and c.cpu().tolist() == [k << 14] * (m * n), route
+    assert route["tile_n"] == (16 if k <= (1 << 18) else 32), route
+
+
+
+@pytest.mark.parametrize("m,k,n", [(8, 4096, 8192 - 5), (20, 2048, 12288 + 3), (13, 2048, 32768),
+                                   (32, 2048, 28672), (5, 6144, 16 * 256 * 5 + 9), (32, 2048, 64)])
+def test_tiles_per_cu(uor, dev, m, k, n):
+    """The LDS-activation kernel (4 < m <= 32) with 2, 4, 8, 7, 6 and 1
+    sixteen-column tiles per CU (ragged n, one row block or two, one to three
+    activation chunks), against a decode in torch plus a float64 matmul
+    (exact: every sum is an integer below 2^53)."""
+    group = 128
+    rng = np.random.default_rng(m + k + n)
+    a = to_dev(rng.integers(-128, 128, m * k).astype(np.int8), dev)
+    codes = to_dev(rng.integers(0, 256, n * k // 2).astype(np.uint8), dev)
+    books = to_dev(rng.integers(-128, 128, ((n + group - 1) // group) * 16).astype(np.int8), dev)
+    c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1))
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "lut4_mfma" and route["split_k"] == 1, route
+    W = decode_torch(codes, n, k, books, group).to(torch.float64)
+    want = a.view(m, k).to(torch.float64) @ W.T
+    assert torch.equal(c.view(m, n).to(torch.float64), want), route

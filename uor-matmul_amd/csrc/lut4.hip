@@ -22,6 +22,7 @@
 // them: every code byte is read from HBM exactly once.
 
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -360,6 +361,16 @@ static unsigned resident_blocks(K kern) {
     return (unsigned)(per * cus);
 }
 
+static int device_cus_lut() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        return n;
+    }();
+    return cus;
+}
+
 static int lut_variant() {
     static int v = [] {
         const char *e = getenv("UOR_GFX950_LUT_VARIANT");
@@ -441,6 +452,274 @@ __global__ void __launch_bounds__(256) lut4_mfma_kernel(LutArgs L, int fast, int
     }
 }
 
+// ------------------------------- 4 < m <= 64: 16-column MFMA tiles, k/4
+//
+// A workgroup of four waves owns 16 coded rows (output columns) j0..j0+15;
+// wave w sums the w-th quarter of the 128-weight steps.  Per step, lane
+// (c = l%16, g = l/16) loads the 16 code bytes of column j0+c covering weights
+// [32g, 32g+32) of the step (one 16-byte load; a column's 64 bytes per step
+// are contiguous), decodes them and interleaves the even/odd halves back into
+// natural k order, giving two v_mfma_i32_16x16x64_i8 A operands (weights
+// 32g..+16 and 32g+16..+32).  The B operands are the activations of rows
+// 16b + c at the same k, two 16-byte loads per row block, used as they lie in
+// memory.  Lane l of a 16x16 result holds row 4(l/16)+i (an output column) and
+// column l%16 (an activation row).  The four quarters meet in LDS as exact
+// i64 sums (each quarter's i32 partial is below 2^30: at most 65536 weights).
+template <int MB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7, 8)))
+lut4_mfma16_kernel(LutArgs L, int book_aligned, uint64_t qsteps) {
+    __shared__ v4i red[3][MB][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const uint64_t j0 = (uint64_t)blockIdx.x * 16;
+    const uint64_t j = j0 + c;
+    const uint64_t jl = j < L.n ? j : L.n - 1;  // columns past n load a valid row, discarded
+    const uint64_t nsteps = L.k / 128;
+    const uint64_t s0 = (uint64_t)wave * qsteps;
+    const uint64_t s1 = min(nsteps, s0 + qsteps);
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+
+    uint32_t q0, q1, q2, q3;
+    load_book(L, jl, book_aligned, q0, q1, q2, q3);
+    const uint8_t *cp = L.codes + jl * L.half + 16 * g;
+    // Rows past m read row 0 (their products land in result columns that are
+    // never stored), so every load is unconditional and the activation loads
+    // of a step are all in flight before its decode.
+    const int8_t *ap[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        const uint64_t r = 16 * b + c;
+        ap[b] = L.a + (int64_t)(r < L.m ? r : 0) * L.ars + 32 * g;
+    }
+    v4i acc[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[b] = v4i{};
+
+    auto step = [&](uint64_t st, const uint4 &cw) {
+        v4i x0[MB], x1[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const int8_t *p = ap[b] + st * 128;
+            x0[b] = *(const v4i *)p;
+            x1[b] = *(const v4i *)(p + 16);
+        }
+        uint32_t e[4], o[4];
+        decode8(cw.x, q0, q1, q2, q3, m4, id, e[0], o[0]);
+        decode8(cw.y, q0, q1, q2, q3, m4, id, e[1], o[1]);
+        decode8(cw.z, q0, q1, q2, q3, m4, id, e[2], o[2]);
+        decode8(cw.w, q0, q1, q2, q3, m4, id, e[3], o[3]);
+        // Natural order: [w0 w1 w2 w3] = e0 o0 e1 o1 bytes 0,0,1,1 ...
+        const v4i w01 = v4i{(int)perm(o[0], e[0], 0x05010400u), (int)perm(o[0], e[0], 0x07030602u),
+                            (int)perm(o[1], e[1], 0x05010400u), (int)perm(o[1], e[1], 0x07030602u)};
+        const v4i w23 = v4i{(int)perm(o[2], e[2], 0x05010400u), (int)perm(o[2], e[2], 0x07030602u),
+                            (int)perm(o[3], e[3], 0x05010400u), (int)perm(o[3], e[3], 0x07030602u)};
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w01, x0[b], acc[b], 0, 0, 0);
+            acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w23, x1[b], acc[b], 0, 0, 0);
+        }
+    };
+    // U steps of codes in flight per wave (fewer with more row blocks, so the
+    // kernel stays within the 72 registers of seven waves per SIMD).
+    constexpr int U = MB == 1 ? 4 : 2;
+    uint64_t st = s0;
+    for (; st + U <= s1; st += U) {
+        uint4 cw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) cw[u] = *(const uint4 *)(cp + (st + u) * 64);
+#pragma unroll
+        for (int u = 0; u < U; ++u) step(st + u, cw[u]);
+    }
+    for (; st < s1; ++st) step(st, *(const uint4 *)(cp + st * 64));
+
+    if (wave > 0) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) red[wave - 1][b][lane] = acc[b];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        const uint64_t r = 16 * b + c;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t col = j0 + 4 * g + i;
+            const int64_t sum = (int64_t)acc[b][i] + red[0][b][lane][i] + red[1][b][lane][i] + red[2][b][lane][i];
+            if (r < L.m && col < L.n) lut_finish_any(L, r, col, sum);
+        }
+    }
+}
+
+// ------------------------ m <= 32, one workgroup per CU, activations in LDS
+//
+// The workgroup owns T consecutive 16-column tiles (T = tiles per CU), one
+// wave per tile over the whole depth (more than 16 tiles: rounds of W), so no
+// partial sums cross waves.  Per 128-weight step, lane (c = l%16, g = l/16)
+// loads the 16 code bytes of column j0+c covering weights [32g, 32g+32) of
+// the step (a column's 64 bytes per step are contiguous) and decodes them
+// into two v_mfma_i32_16x16x64_i8 A operands, in the decode's own order:
+// per 8 weights the even ones, then the odd ones.  The activations are what
+// the waves share: they pass through LDS in chunks of KC weights (16*MB rows
+// x KC bytes, double-buffered), read from global memory once per workgroup in
+// coalesced 1 KiB pieces (one row's 1024 consecutive weights) and stored in
+// that same even/odd order, so each B operand is one ds_read_b128 and needs
+// no rearranging.  Chunk c+1's pieces are loaded during chunk c, one per wave
+// per step, and written PD = 8 steps later; a barrier closes each chunk.
+// Codes are loaded CR = 16 steps ahead through a buffer resource, so the
+// loads past the last step read zeros instead of leaving the buffer.  (Loads
+// retire in order, so a piece's write waits for every code load issued before
+// it: the write delay bounds how far ahead the codes really are.)
+//
+// LDS layout of a chunk buffer: row r, 16-byte chunk x at r*KC + 16*(x ^ (r & 15)),
+// so the 16 rows a B-operand read touches sit on distinct banks.  Everything
+// about a piece except the lane's 16 bytes is wave-uniform (scalar); pieces
+// outside the set read a valid place and write a dummy slot, so every step
+// has the same instructions.
+template <int MB>
+__global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_aligned, uint32_t tpw) {
+    constexpr int CR = 16, PD = 8;  // code ring (steps ahead), piece write delay
+    constexpr int ROWS = 16 * MB;
+    constexpr int KC = 4096 / MB;  // weights per chunk
+    constexpr int S = KC / 128;    // steps per chunk
+    constexpr int PPR = KC / 1024; // pieces per row per chunk
+    constexpr int CB = ROWS * KC;  // bytes per chunk buffer (64 KiB)
+    static_assert(S % CR == 0 && PPR >= 1, "chunk shape");
+    __shared__ __attribute__((aligned(16))) int8_t abuf[2 * CB + 1024];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = blockDim.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const uint64_t nsteps = L.k / 128, nchunks = (L.k + KC - 1) / KC;
+    const uint64_t ntiles = (L.n + 15) / 16;
+    const uint64_t t0 = (uint64_t)blockIdx.x * tpw, t1 = min(t0 + tpw, ntiles);
+    const int P = (int)L.m * PPR;  // pieces per full chunk
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)abuf;
+    typedef __attribute__((address_space(3))) v4i lds_v4i;
+    typedef __attribute__((address_space(3))) const v4i lds_v4i_c;
+
+    // Piece q of chunk ch (wave-uniform): row q / PPR, weights ch*KC +
+    // (q % PPR)*1024 + 16*lane ..; lane L's 16-byte chunk x = (q % PPR)*64 + L
+    // lands at row*KC + 16*(x ^ (row & 15)) = ... + 16*(L ^ (row & 15)).
+    auto piece_load = [&](uint64_t ch, int q, uint32_t &dst) -> v4i {
+        const int row = q / PPR, part = q % PPR;
+        const uint64_t kb = ch * KC + (uint64_t)part * 1024;
+        const bool ok = q < P && ch < nchunks && kb < L.k;
+        const int8_t *src = ok ? L.a + (int64_t)row * L.ars + (int64_t)kb : L.a;
+        dst = ok ? (uint32_t)(row * KC + part * 1024) + 16u * (uint32_t)(lane ^ (row & 15)) : (uint32_t)(2 * CB) + 16u * lane;
+        const v4i x = *(const v4i *)(src + 16 * lane);
+        // The decode's order: per 8 weights the even ones, then the odd ones.
+        return v4i{(int)perm((uint32_t)x[1], (uint32_t)x[0], 0x06040200u), (int)perm((uint32_t)x[1], (uint32_t)x[0], 0x07050301u),
+                   (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x06040200u), (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x07050301u)};
+    };
+    auto piece_store = [&](int buf, uint32_t dst, const v4i &v) {
+        const uint32_t off = dst < (uint32_t)(2 * CB) ? dst + (uint32_t)(buf * CB) : dst;
+        *(lds_v4i *)(uintptr_t)(lds0 + off) = v;
+    };
+    // B-operand read offsets: weights 128*sl + 32g + [0,16) are chunk
+    // x = 8sl + 2g, at 256*(sl >> 1) + 16*((8*(sl & 1) + 2g) ^ c) in the row
+    // (c = row & 15); the next 16 weights are chunk x + 1.
+    uint32_t boff[2][2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) boff[p][h] = lds0 + (uint32_t)(c * KC) + 16u * (uint32_t)((8 * p + 2 * g + h) ^ c);
+    // Codes through a buffer resource (the host checks that they lie below 2^31 bytes).
+    const __amdgpu_buffer_rsrc_t crs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)L.codes, 0, (int)min(L.n * L.half, (uint64_t)0x7FFFFFFF), 0x00020000);
+
+    const int rounds = (int)((tpw + W - 1) / W);
+    for (int rd = 0; rd < rounds; ++rd) {
+        const uint64_t tile = t0 + (uint64_t)rd * W + wave;
+        const bool active = tile < t1;
+        const uint64_t j0 = (active ? tile : t0) * 16;
+        const uint64_t j = j0 + c;
+        const uint64_t jl = j < L.n ? j : L.n - 1;
+        uint32_t q0, q1, q2, q3;
+        load_book(L, jl, book_aligned, q0, q1, q2, q3);
+        const uint32_t cvo = (uint32_t)(jl * L.half) + 16u * g;  // this lane's code offset at step 0
+
+        // Chunk 0's pieces, then the first CR steps of codes.
+        for (int q = wave; q < P; q += W) {
+            uint32_t dst;
+            const v4i v = piece_load(0, q, dst);
+            piece_store(0, dst, v);
+        }
+        v4i ring[CR];
+#pragma unroll
+        for (int u = 0; u < CR; ++u) ring[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(crs, cvo, u * 64, 0));
+        __syncthreads();
+
+        v4i acc[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[b] = v4i{};
+        v4i pr[PD];
+        uint32_t pdst[PD];
+#pragma unroll
+        for (int t = 0; t < PD; ++t) pr[t] = v4i{}, pdst[t] = (uint32_t)(2 * CB);
+        for (uint64_t ch = 0; ch < nchunks; ++ch) {
+            const int cur = (int)(ch & 1), nxt = cur ^ 1;
+            const uint64_t sbeg = ch * S, send = min(nsteps, sbeg + S);
+            for (uint64_t s8 = sbeg; s8 < send; s8 += CR) {
+                const uint32_t cb_off = (uint32_t)(cur * CB) + 128u * (uint32_t)(s8 - sbeg);
+#pragma unroll
+                for (int u = 0; u < CR; ++u) {
+                    const uint64_t st = s8 + u;
+                    const int sl = (int)(s8 - sbeg) + u;
+                    // The next chunk's pieces: write the one loaded PD steps
+                    // ago (in this chunk), load one.
+                    piece_store(nxt, sl >= PD ? pdst[u % PD] : (uint32_t)(2 * CB), pr[u % PD]);
+                    pr[u % PD] = piece_load(ch + 1, sl * W + wave, pdst[u % PD]);
+                    // Codes of step st, and the load of step st + CR.
+                    const v4i cw = ring[u];
+                    ring[u] = __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(crs, cvo, (int)((st + CR) * 64), 0));
+                    // B operands from LDS.
+                    v4i x0[MB], x1[MB];
+#pragma unroll
+                    for (int b = 0; b < MB; ++b) {
+                        const uint32_t ro = cb_off + 256u * (uint32_t)(u >> 1) + (uint32_t)(16 * b * KC);
+                        x0[b] = *(lds_v4i_c *)(uintptr_t)(boff[u & 1][0] + ro);
+                        x1[b] = *(lds_v4i_c *)(uintptr_t)(boff[u & 1][1] + ro);
+                    }
+                    uint32_t e[4], o[4];
+                    decode8((uint32_t)cw[0], q0, q1, q2, q3, m4, id, e[0], o[0]);
+                    decode8((uint32_t)cw[1], q0, q1, q2, q3, m4, id, e[1], o[1]);
+                    decode8((uint32_t)cw[2], q0, q1, q2, q3, m4, id, e[2], o[2]);
+                    decode8((uint32_t)cw[3], q0, q1, q2, q3, m4, id, e[3], o[3]);
+                    const v4i w01 = v4i{(int)e[0], (int)o[0], (int)e[1], (int)o[1]};
+                    const v4i w23 = v4i{(int)e[2], (int)o[2], (int)e[3], (int)o[3]};
+#pragma unroll
+                    for (int b = 0; b < MB; ++b) {
+                        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w01, x0[b], acc[b], 0, 0, 0);
+                        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w23, x1[b], acc[b], 0, 0, 0);
+                    }
+                }
+            }
+            // The last PD pieces of the next chunk (the chunk's step count is
+            // a multiple of CR, so they sit in ring order), then the barrier
+            // that closes this chunk (its reads done, the next one written).
+#pragma unroll
+            for (int t = 0; t < PD; ++t) {
+                piece_store(nxt, pdst[t], pr[t]);
+                pdst[t] = (uint32_t)(2 * CB);
+            }
+            __syncthreads();
+        }
+        if (active) {
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                const uint64_t r = 16 * b + c;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint64_t col = j0 + 4 * g + i;
+                    if (r < L.m && col < L.n) lut_finish_any(L, r, col, (int64_t)acc[b][i]);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace uor
 
 using namespace uor;
@@ -489,6 +768,32 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         route->launches = 1;
         route->operand_modes = fast;
     }
+    const bool a16 = A.cs == 1 && ((uintptr_t)A.base % 16 == 0) && (A.rs % 16 == 0 || m == 1);
+    // 4 < m <= 32, whole 2048-weight blocks, k <= 65536 (each wave's i32 sum
+    // over the whole depth is exact), 16-byte aligned code rows (all below
+    // 2^31 bytes) and activation rows: one workgroup per CU with the
+    // activations in LDS.  Its waves must cover a chunk's m*KC/1024 pieces at
+    // one per wave per step: W >= m/8.  (For m <= 4 the dot4 kernels below
+    // are faster: 28 us against 33 us at m = 1, k = 8192, n = 28672.)
+    if (m > 4 && m <= 32 && k % 2048 == 0 && k <= 65536 && code_fast && a16 && n * (k / 2) < (1ull << 31) &&
+        lut_variant() == 1) {
+        const uint64_t ntiles = (n + 15) / 16;
+        const uint64_t cus = (uint64_t)device_cus_lut();
+        const uint64_t tpw = (ntiles + cus - 1) / cus;
+        uint64_t w = tpw < 8 ? tpw : 8;
+        const uint64_t wmin = (m + 7) / 8;
+        if (w < wmin) w = wmin;
+        const uint64_t blocks = (ntiles + tpw - 1) / tpw;
+        if (blocks <= 0x7FFFFFFFull && tpw <= 0xFFFFFFFFull) {
+            const int mb = (int)((m + 15) / 16);
+            if (route) route->tile_m = 16 * mb, route->tile_n = 16, route->split_k = 1, route->kind = UOR_ROUTE_LUT4_MFMA;
+            const dim3 grid((unsigned)blocks), block((unsigned)(64 * w));
+            if (mb == 1) hipLaunchKernelGGL((lut4_lds_kernel<1>), grid, block, 0, s, L, book_aligned, (uint32_t)tpw);
+            else hipLaunchKernelGGL((lut4_lds_kernel<2>), grid, block, 0, s, L, book_aligned, (uint32_t)tpw);
+            UOR_HIP(hipGetLastError());
+            return UOR_OK;
+        }
+    }
     if (m <= 4 && k <= 65536) {
         // 4096 persistent waves (four per SIMD), each walking columns j,
         // j + W, ...: a sweep of 2048..14336 on MI355X put the optimum here.
@@ -520,12 +825,30 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         UOR_HIP(hipGetLastError());
         return UOR_OK;
     }
+    // 4 < m <= 64 with whole 128-weight steps, 16-byte aligned code rows and
+    // 16-byte activation rows: the 16-column tiles.  A quarter holds at most
+    // 512 steps (65536 weights), so its i32 partial is exact.
+    if (m <= 64 && k % 128 == 0 && k <= 4 * 65536 && code_fast && a16) {
+        const uint64_t nsteps = k / 128, qsteps = (nsteps + 3) / 4;
+        const uint64_t tiles = (n + 15) / 16;
+        if (tiles > 0x7FFFFFFFull) return UOR_INVALID_ARGUMENT;
+        const int mb = (int)((m + 15) / 16);
+        if (route) route->tile_m = 16 * mb, route->tile_n = 16, route->split_k = 4, route->kind = UOR_ROUTE_LUT4_MFMA;
+        switch (mb) {
+        case 1: hipLaunchKernelGGL((lut4_mfma16_kernel<1>), dim3((unsigned)tiles), dim3(256), 0, s, L, book_aligned, qsteps); break;
+        case 2: hipLaunchKernelGGL((lut4_mfma16_kernel<2>), dim3((unsigned)tiles), dim3(256), 0, s, L, book_aligned, qsteps); break;
+        case 3: hipLaunchKernelGGL((lut4_mfma16_kernel<3>), dim3((unsigned)tiles), dim3(256), 0, s, L, book_aligned, qsteps); break;
+        default: hipLaunchKernelGGL((lut4_mfma16_kernel<4>), dim3((unsigned)tiles), dim3(256), 0, s, L, book_aligned, qsteps); break;
+        }
+        UOR_HIP(hipGetLastError());
+        return UOR_OK;
+    }
     // Quarter of k per wave, in whole 128-weight steps.
     uint64_t kq = (k + 3) / 4;
     kq = (kq + 127) / 128 * 128;
     if (kq == 0) kq = 128;
     const uint64_t tiles = ((n + 31) / 32) * ((m + 31) / 32);
-    if (route) route->tile_m = 32, route->tile_n = 32, route->split_k = 4;
+    if (route) route->tile_m = 32, route->tile_n = 32, route->split_k = 4, route->kind = UOR_ROUTE_LUT4_MFMA;
     if (tiles > 0x7FFFFFFFull) return UOR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(lut4_mfma_kernel, dim3((unsigned)tiles), dim3(256), 0, s, L, fast, book_aligned, kq);
     UOR_HIP(hipGetLastError());

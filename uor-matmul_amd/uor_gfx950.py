@@ -22,7 +22,7 @@ ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
           4: "invalid_argument"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
-          10: "lut4_dot4", 20: "float_crt", 21: "float_direct", 30: "trop_valu"}
+          10: "lut4_dot4", 11: "lut4_mfma", 20: "float_crt", 21: "float_direct", 30: "trop_valu"}
 
 # Every symbol include/uor_gfx950.h declares.
 SYMBOLS = [
