@@ -63,6 +63,15 @@ def settle(torch, step, seconds=SETTLE_S):
     return n
 
 
+def i8_kernel_name():
+    """The 256x256 kernel the headline runs (UOR_GFX950_DL_VARIANT, read by
+    the library at load time; s4 unless set)."""
+    v = os.environ.get("UOR_GFX950_DL_VARIANT", "s4")
+    return {"w8": "gemm_i8_dl_kernel<256,256,2,4,FUSED,FAST,i32>",
+            "w8pf": "gemm_i8_dl_kernel<256,256,2,4,FUSED,FAST,i32,prefetch>",
+            "w4": "gemm_i8_dl_kernel<256,256,2,2,FUSED,FAST,i32>"}.get(v, "gemm_i8_s4_kernel<FAST,i32>")
+
+
 def load_traffic(name):
     p = ROOT / "profiles" / f"{name}.traffic.json"
     if p.exists():
@@ -147,7 +156,7 @@ def bench_i8(args, torch, uor, gen):
         "wall_s": round(wall, 4),
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_i8_dl_kernel<256,256,2,4,FUSED,FAST,i32>",
+            "kernel": i8_kernel_name(),
             "achieved": round(tops, 2),
             "peak": PEAK_INT8_TOPS,
             "unit": "TFLOP/s",
@@ -157,7 +166,7 @@ def bench_i8(args, torch, uor, gen):
         },
     }
     t = load_traffic("gemm_i8_8192")
-    if t:
+    if t and t.get("kernel") == result["roofline"]["kernel"]:
         result["roofline"]["traffic"] = t.get("bytes_per_launch")
     return result, (a, b, c0)
 
