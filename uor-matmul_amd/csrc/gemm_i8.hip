@@ -694,8 +694,12 @@ __device__ inline void s4_epilogue_full(const OutArgs &out, const v16i (&acc)[4]
     typedef typename std::conditional<OB == 8, int64_t, int32_t>::type P;
     constexpr int NB = OB == 8 ? 1 : 2;  // prior batches in flight
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(corner, 0, 0x7FFFFFFF, 0x00020000);
+    // The row stride passes through an empty asm per use, so each offset is
+    // formed next to its access instead of all 256 being held in SGPRs.
     auto offs = [&](int i, int j, int r) -> int {
-        return (32 * i + 8 * (r >> 2) + (r & 3)) * srs + (32 * j) * scs;
+        int rs_ = srs;
+        asm volatile("" : "+s"(rs_));
+        return (32 * i + 8 * (r >> 2) + (r & 3)) * rs_ + (32 * j) * scs;
     };
     P pr[NB][4][16];
     auto load = [&](int i, P (&p)[4][16]) {
@@ -766,7 +770,10 @@ gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
     int tile = blockIdx.x;
     if (tile >= ntiles) return;
     const int nk = (int)(K / DL_BK);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // (The wave index through readfirstlane: the compiler then knows every
+    // block corner, and so every buffer resource the epilogue builds, is
+    // uniform, instead of looping over lanes for each access.)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, l32 = lane & 31;
 
