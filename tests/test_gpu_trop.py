@@ -128,3 +128,21 @@ def test_config5_4096(oracle, uor, dev):
         oracle.gemm_trop(a[2 * r * N:2 * (r + 1) * N].copy(), (1, N), (N, 1), b, (N, N), (N, 1),
                          cr, (1, N), (N, 1))
         assert np.array_equal(cr.view(REC[4])["value"], got["value"][r * N:(r + 1) * N])
+
+
+@pytest.mark.parametrize("shape", [(8, 8, 8), (136, 200, 264), (1000, 96, 136), (129, 1000, 520),
+                                   (5, 4104, 16)])
+@pytest.mark.parametrize("ob", [1, 4])
+def test_record_vector_loads(oracle, uor, dev, shape, ob):
+    """Unit record strides, k and n multiples of 8: the 16-byte record loads
+    (ragged m and n tiles, k tails shorter than a 32-deep step), against the
+    oracle, with alpha/beta finite and a prior C."""
+    m, k, n = shape
+    rng = np.random.default_rng(m * 5 + k * 3 + n + ob)
+    a = rand_trop(rng, m * k, p_inf=0.1)
+    b = rand_trop(rng, k * n, p_inf=0.1)
+    c0 = np.zeros(m * n, REC[ob])
+    c0["value"] = rng.integers(-100, 100, m * n)
+    c0["finite"] = rng.random(m * n) < 0.5
+    check(oracle, uor, dev, a, (m, k), (k, 1), b, (k, n), (n, 1), c0.view(np.uint8).copy(), (m, n), (n, 1),
+          ob=ob, alpha=(3, True), beta=(-2, True), encode="nearest" if ob == 4 else "wrapping")

@@ -92,6 +92,53 @@ __device__ inline void trop_finish(const TropArgs &T, uint64_t i, uint64_t j, in
     else trop_store<OB>(cp, false, 0);
 }
 
+// Eight Trop<i8> records (16 bytes) -> eight i16 operands, two per dword
+// (value when the finite byte is nonzero, NEG otherwise).
+__device__ inline v4i trop16x8(const v4i &r) {
+    v4i o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t x = (uint32_t)r[d];
+        const int lo = (x & 0x0000FF00u) ? (int)(int8_t)(x & 0xFF) : (int)NEG;
+        const int hi = (x & 0xFF000000u) ? (int)(int8_t)((x >> 16) & 0xFF) : (int)NEG;
+        o[d] = (int)(((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16));
+    }
+    return o;
+}
+
+// The inner product of one staged k-step: 8 x 8 cells per thread.
+__device__ inline void trop_step(const short *As, const short *Bs, int ty, int tx, s2 (&acc)[8][8]) {
+#pragma unroll
+    for (int p0 = 0; p0 < TK; p0 += 8) {
+        v4i av[8], bv[8];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) av[a] = *(const v4i *)(As + (ty + 16 * a) * TSTR + p0);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) bv[b] = *(const v4i *)(Bs + (tx + 16 * b) * TSTR + p0);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    // Copy the lanes out before the cast: a bit_cast of a
+                    // vector-subscript lvalue reads element 0 under this
+                    // compiler, whatever the subscript.
+                    const int xa = av[a][d], yb = bv[b][d];
+                    const s2 x = __builtin_bit_cast(s2, xa);
+                    const s2 y = __builtin_bit_cast(s2, yb);
+                    acc[a][b] = __builtin_elementwise_max(acc[a][b], x + y);
+                }
+    }
+}
+
+// FAST: unit record strides along k (A) and n (B), 16-byte aligned rows, k
+// and n multiples of 8 (the host checks).  Each k-step's records arrive as
+// 16-byte loads of 8 records (two per operand per thread) instead of one
+// 2-byte record per load.  (Loading the next step before this step's products,
+// into double-buffered LDS, needs 16 more registers than the products leave:
+// it spilled.)
+template <bool FAST>
 __global__ void __launch_bounds__(256) trop_i8_kernel(TropArgs T, int gm, int gn) {
     __shared__ __attribute__((aligned(16))) short As[TB * TSTR];
     __shared__ __attribute__((aligned(16))) short Bs[TB * TSTR];
@@ -106,6 +153,44 @@ __global__ void __launch_bounds__(256) trop_i8_kernel(TropArgs T, int gm, int gn
 #pragma unroll
         for (int b = 0; b < 8; ++b) acc[a][b] = s2{-32768, -32768};
 
+    if constexpr (FAST) {
+        // A chunk q = t + 256h: row q/4, records k0 + 8(q%4) ..; B chunk:
+        // k-row q/16, columns n0 + 8(q%16) ..  Missing records read as zero
+        // bytes, i.e. not finite.
+        v4i ra[2], rb[2];
+        auto gload = [&](uint64_t k0) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int q = t + 256 * h;
+                const uint64_t gi = m0 + (q >> 2), gk = k0 + 8 * (q & 3);
+                ra[h] = (gi < T.m && gk < T.k) ? *(const v4i *)(T.a + ((int64_t)gi * T.ars + (int64_t)gk) * 2) : v4i{};
+                const uint64_t gr = k0 + (q >> 4), gj = n0 + 8 * (q & 15);
+                rb[h] = (gr < T.k && gj < T.n) ? *(const v4i *)(T.b + ((int64_t)gr * T.brs + (int64_t)gj) * 2) : v4i{};
+            }
+        };
+        auto lstore = [&]() {
+            short *as = As, *bs = Bs;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int q = t + 256 * h;
+                *(v4i *)(as + (q >> 2) * TSTR + 8 * (q & 3)) = trop16x8(ra[h]);
+                const v4i v = trop16x8(rb[h]);
+                const int kr = q >> 4, c8 = 8 * (q & 15);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t w = (uint32_t)v[i >> 1];
+                    bs[(c8 + i) * TSTR + kr] = (short)((i & 1) ? (w >> 16) : (w & 0xFFFF));
+                }
+            }
+        };
+        for (uint64_t k0 = 0; k0 < T.k; k0 += TK) {
+            gload(k0);
+            lstore();
+            __syncthreads();
+            trop_step(As, Bs, ty, tx, acc);
+            __syncthreads();
+        }
+    } else
     for (uint64_t k0 = 0; k0 < T.k; k0 += TK) {
         // A tile: 128 rows x 32 k; consecutive threads walk k.
 #pragma unroll 4
@@ -127,28 +212,7 @@ __global__ void __launch_bounds__(256) trop_i8_kernel(TropArgs T, int gm, int gn
                                      : NEG;
         }
         __syncthreads();
-#pragma unroll
-        for (int p0 = 0; p0 < TK; p0 += 8) {
-            v4i av[8], bv[8];
-#pragma unroll
-            for (int a = 0; a < 8; ++a) av[a] = *(const v4i *)(As + (ty + 16 * a) * TSTR + p0);
-#pragma unroll
-            for (int b = 0; b < 8; ++b) bv[b] = *(const v4i *)(Bs + (tx + 16 * b) * TSTR + p0);
-#pragma unroll
-            for (int d = 0; d < 4; ++d)
-#pragma unroll
-                for (int a = 0; a < 8; ++a)
-#pragma unroll
-                    for (int b = 0; b < 8; ++b) {
-                        // Copy the lanes out before the cast: a bit_cast of a
-                        // vector-subscript lvalue reads element 0 under this
-                        // compiler, whatever the subscript.
-                        const int xa = av[a][d], yb = bv[b][d];
-                        const s2 x = __builtin_bit_cast(s2, xa);
-                        const s2 y = __builtin_bit_cast(s2, yb);
-                        acc[a][b] = __builtin_elementwise_max(acc[a][b], x + y);
-                    }
-        }
+        trop_step(As, Bs, ty, tx, acc);
         __syncthreads();
     }
 
@@ -202,8 +266,18 @@ extern "C" int uor_gfx950_gemm_trop_i8(const uor_view *a, const uor_view *b, con
         route->split_k = 1;
         route->launches = 1;
     }
-    hipLaunchKernelGGL(trop_i8_kernel, dim3((unsigned)(gm * gn)), dim3(256), 0, (hipStream_t)stream,
-                       T, (int)gm, (int)gn);
+    // 16-byte record loads: unit record strides, 16-byte aligned bases and
+    // rows, k and n multiples of 8 records.
+    const bool fast = T.acs == 1 && T.bcs == 1 && ((((uintptr_t)T.a) | ((uintptr_t)T.b)) & 15) == 0 &&
+                      T.ars > 0 && T.brs > 0 && (T.ars % 8) == 0 && (T.brs % 8) == 0 && T.k % 8 == 0 &&
+                      T.n % 8 == 0;
+    if (route) route->operand_modes = fast ? 1 : 0;
+    if (fast)
+        hipLaunchKernelGGL((trop_i8_kernel<true>), dim3((unsigned)(gm * gn)), dim3(256), 0, (hipStream_t)stream,
+                           T, (int)gm, (int)gn);
+    else
+        hipLaunchKernelGGL((trop_i8_kernel<false>), dim3((unsigned)(gm * gn)), dim3(256), 0, (hipStream_t)stream,
+                           T, (int)gm, (int)gn);
     UOR_HIP(hipGetLastError());
     return UOR_OK;
 }
