@@ -338,3 +338,27 @@ def test_tile256_ragged_edges_and_depths(uor, dev, m, n, k):
     got = c.cpu().numpy().reshape(m, ldc)
     assert np.array_equal(got[:, :n].astype(np.int64), want)
     assert np.array_equal(got[:, n:], c0.reshape(m, ldc)[:, n:])
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 8192 + 64, 128), (200, 2 * 65536 + 192, 144),
+                                   (64, 262144 + 64, 48)])
+def test_splitk_interleaved_steps(uor, dev, m, k, n):
+    """Split-K on the 128-wide direct-to-LDS tile (k % 64 == 0, n % 16 == 0):
+    split z sums the 64-deep steps z, z + splits, z + 2*splits, ...  The step
+    counts (129 over 65 splits, 2051 over 206, 4097 over 683) leave some
+    splits one step short, and m, n leave partial edge tiles.  Random i8
+    operands, i64 output with alpha = 3, beta = -1; expected values from an
+    exact float64 product (|sum| <= k * 2^14 < 2^53)."""
+    rng = np.random.default_rng(m + 3 * n + 5 * k)
+    a = torch.from_numpy(rng.integers(-128, 128, m * k).astype(np.int8)).to(dev)
+    b = torch.from_numpy(rng.integers(-128, 128, k * n).astype(np.int8)).to(dev)
+    c0 = rng.integers(-(1 << 40), 1 << 40, m * n).astype(np.int64)
+    c = torch.from_numpy(c0.copy()).to(dev)
+    scratch = torch.empty(uor.suggested_scratch_i8(m, k, n), dtype=torch.uint8, device=dev)
+    st, route = uor.gemm_i8(a, (m, k), (k, 1), b, (k, n), (n, 1), c, (m, n), (n, 1), out="i64",
+                            alpha=3, beta=-1, scratch=scratch)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_splitk" and route["tile_m"] == 128, route
+    S = (a.view(m, k).double() @ b.view(k, n).double()).cpu().numpy().astype(np.int64)
+    want = 3 * S - c0.reshape(m, n)
+    assert np.array_equal(c.cpu().numpy().reshape(m, n), want)

@@ -433,12 +433,19 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
     int tm, tn;
     tile_of(gm, gn, &tm, &tn);
     const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
-    uint64_t kbeg = 0, kend = K;
+    // A reduction split takes every splits-th 64-deep step, starting at its own
+    // index: at any moment the resident splits read neighbouring 64-byte
+    // pieces of every A row (one long run per row across the device) instead
+    // of one piece from each of their distant slices.  A split sums at most
+    // ceil(kslice / 64) steps, so its i32 lanes stay exact.
+    uint64_t kbeg = 0, kstep = DL_BK;
+    int nk = (int)(K / DL_BK);
     if constexpr (EPI == EPI_PARTIAL) {
-        kbeg = (uint64_t)blockIdx.z * kslice;
-        kend = kbeg + kslice < K ? kbeg + kslice : K;
+        const uint64_t steps = K / DL_BK, z = blockIdx.z, splits = gridDim.z;
+        kbeg = z * DL_BK;
+        kstep = splits * DL_BK;
+        nk = z < steps ? (int)((steps - z + splits - 1) / splits) : 0;
     }
-    const int nk = (int)((kend - kbeg) / DL_BK);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -450,8 +457,8 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
-    if constexpr (PF) dl_mainloop_pf<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc);
-    else dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc);
+    if constexpr (PF) dl_mainloop_pf<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc, kstep);
+    else dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc, kstep);
     __syncthreads();
 
     if constexpr (EPI == EPI_FUSED && FAST && OB <= 4 && WM * WN == 8 && FM * FN == 8) {

@@ -607,13 +607,15 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
         const bool ok = q < P && ch < nchunks && kb < L.k;
         const int8_t *src = ok ? L.a + (int64_t)row * L.ars + (int64_t)kb : L.a;
         dst = ok ? (uint32_t)(row * KC + part * 1024) + 16u * (uint32_t)(lane ^ (row & 15)) : (uint32_t)(2 * CB) + 16u * lane;
-        const v4i x = *(const v4i *)(src + 16 * lane);
-        // The decode's order: per 8 weights the even ones, then the odd ones.
-        return v4i{(int)perm((uint32_t)x[1], (uint32_t)x[0], 0x06040200u), (int)perm((uint32_t)x[1], (uint32_t)x[0], 0x07050301u),
-                   (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x06040200u), (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x07050301u)};
+        return *(const v4i *)(src + 16 * lane);
     };
-    auto piece_store = [&](int buf, uint32_t dst, const v4i &v) {
+    // Stored in the decode's order: per 8 weights the even ones, then the odd
+    // ones.  (The rearranging happens here, at the store, so a load's first
+    // use is the store that comes PD steps later.)
+    auto piece_store = [&](int buf, uint32_t dst, const v4i &x) {
         const uint32_t off = dst < (uint32_t)(2 * CB) ? dst + (uint32_t)(buf * CB) : dst;
+        const v4i v = v4i{(int)perm((uint32_t)x[1], (uint32_t)x[0], 0x06040200u), (int)perm((uint32_t)x[1], (uint32_t)x[0], 0x07050301u),
+                          (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x06040200u), (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x07050301u)};
         *(lds_v4i *)(uintptr_t)(lds0 + off) = v;
     };
     // B-operand read offsets: weights 128*sl + 32g + [0,16) are chunk
@@ -639,15 +641,19 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
         load_book(L, jl, book_aligned, q0, q1, q2, q3);
         const uint32_t cvo = (uint32_t)(jl * L.half) + 16u * g;  // this lane's code offset at step 0
 
-        // Chunk 0's pieces, then the first CR steps of codes.
-        for (int q = wave; q < P; q += W) {
-            uint32_t dst;
-            const v4i v = piece_load(0, q, dst);
-            piece_store(0, dst, v);
-        }
+        // The first CR steps of codes, then chunk 0's pieces in batches of
+        // eight per wave, each batch's loads in flight together.
         v4i ring[CR];
 #pragma unroll
         for (int u = 0; u < CR; ++u) ring[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(crs, cvo, u * 64, 0));
+        for (int qb = wave; qb < P; qb += 8 * W) {
+            v4i pv[8];
+            uint32_t pd[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pv[i] = piece_load(0, qb + i * W, pd[i]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) piece_store(0, pd[i], pv[i]);
+        }
         __syncthreads();
 
         v4i acc[MB];
@@ -657,8 +663,10 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
         uint32_t pdst[PD];
 #pragma unroll
         for (int t = 0; t < PD; ++t) pr[t] = v4i{}, pdst[t] = (uint32_t)(2 * CB);
+        static_assert(S % PD == 0, "the chunk's last PD steps sit in ring order");
         for (uint64_t ch = 0; ch < nchunks; ++ch) {
             const int cur = (int)(ch & 1), nxt = cur ^ 1;
+            const bool more = ch + 1 < nchunks;
             const uint64_t sbeg = ch * S, send = min(nsteps, sbeg + S);
             for (uint64_t s8 = sbeg; s8 < send; s8 += CR) {
                 const uint32_t cb_off = (uint32_t)(cur * CB) + 128u * (uint32_t)(s8 - sbeg);
@@ -667,13 +675,12 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
                     const uint64_t st = s8 + u;
                     const int sl = (int)(s8 - sbeg) + u;
                     // The next chunk's pieces: write the one loaded PD steps
-                    // ago (in this chunk), load one.
-                    piece_store(nxt, sl >= PD ? pdst[u % PD] : (uint32_t)(2 * CB), pr[u % PD]);
-                    pr[u % PD] = piece_load(ch + 1, sl * W + wave, pdst[u % PD]);
-                    // Codes of step st, and the load of step st + CR.
+                    // ago (in this chunk), load one.  Steps past the last
+                    // piece load and store nothing (wave-uniform branches).
+                    if (more && sl >= PD && (sl - PD) * W + wave < P) piece_store(nxt, pdst[u % PD], pr[u % PD]);
+                    if (more && sl * W + wave < P) pr[u % PD] = piece_load(ch + 1, sl * W + wave, pdst[u % PD]);
+                    // Codes of step st.
                     const v4i cw = ring[u];
-                    ring[u] = __builtin_bit_cast(
-                        v4i, __builtin_amdgcn_raw_buffer_load_b128(crs, cvo, (int)((st + CR) * 64), 0));
                     // B operands from LDS.
                     v4i x0[MB], x1[MB];
 #pragma unroll
@@ -689,6 +696,13 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
                     decode8((uint32_t)cw[3], q0, q1, q2, q3, m4, id, e[3], o[3]);
                     const v4i w01 = v4i{(int)e[0], (int)o[0], (int)e[1], (int)o[1]};
                     const v4i w23 = v4i{(int)e[2], (int)o[2], (int)e[3], (int)o[3]};
+                    // The load of step st + CR goes into the ring slot just
+                    // read, after the decode: issued earlier, it would need a
+                    // second register set and copies (each waiting for its
+                    // load) on the loop's back edge.
+                    __builtin_amdgcn_sched_barrier(0);
+                    ring[u] = __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(crs, cvo, (int)((st + CR) * 64), 0));
 #pragma unroll
                     for (int b = 0; b < MB; ++b) {
                         acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w01, x0[b], acc[b], 0, 0, 0);
@@ -699,12 +713,17 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
             // The last PD pieces of the next chunk (the chunk's step count is
             // a multiple of CR, so they sit in ring order), then the barrier
             // that closes this chunk (its reads done, the next one written).
+            // The barrier waits for this wave's LDS writes only: the code
+            // loads stay in flight across it.
+            if (more) {
 #pragma unroll
-            for (int t = 0; t < PD; ++t) {
-                piece_store(nxt, pdst[t], pr[t]);
-                pdst[t] = (uint32_t)(2 * CB);
+                for (int t = 0; t < PD; ++t)
+                    if ((S - PD + t) * W + wave < P) piece_store(nxt, pdst[t], pr[t]);
             }
-            __syncthreads();
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
         }
         if (active) {
 #pragma unroll
