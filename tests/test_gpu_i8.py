@@ -344,9 +344,9 @@ def test_tile256_ragged_edges_and_depths(uor, dev, m, n, k):
                                    (64, 262144 + 64, 48)])
 def test_splitk_interleaved_steps(uor, dev, m, k, n):
     """Split-K on the 128-wide direct-to-LDS tile (k % 64 == 0, n % 16 == 0):
-    split z sums the 64-deep steps z, z + splits, z + 2*splits, ...  The step
-    counts (129 over 65 splits, 2051 over 206, 4097 over 683) leave some
-    splits one step short, and m, n leave partial edge tiles.  Random i8
+    split z sums the units of four 64-deep steps z, z + splits, z + 2*splits,
+    ...  The step counts (129, 2051, 4097) end in a short unit and leave some
+    splits a unit short, and m, n leave partial edge tiles.  Random i8
     operands, i64 output with alpha = 3, beta = -1; expected values from an
     exact float64 product (|sum| <= k * 2^14 < 2^53)."""
     rng = np.random.default_rng(m + 3 * n + 5 * k)

@@ -433,18 +433,23 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
     int tm, tn;
     tile_of(gm, gn, &tm, &tn);
     const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
-    // A reduction split takes every splits-th 64-deep step, starting at its own
-    // index: at any moment the resident splits read neighbouring 64-byte
-    // pieces of every A row (one long run per row across the device) instead
-    // of one piece from each of their distant slices.  A split sums at most
-    // ceil(kslice / 64) steps, so its i32 lanes stay exact.
-    uint64_t kbeg = 0, kstep = DL_BK;
+    // A reduction split takes every splits-th unit of DL_UNIT steps (256
+    // bytes of each A row), starting at its own index: the resident splits
+    // read neighbouring pieces of every A row at once, and each 128-byte line
+    // of A is read whole by one split.  With kslice a multiple of 256, a
+    // split sums at most kslice / 64 steps, so its i32 lanes stay exact.
+    uint64_t kbeg = 0, kstep = DL_UNIT * DL_BK;
     int nk = (int)(K / DL_BK);
     if constexpr (EPI == EPI_PARTIAL) {
         const uint64_t steps = K / DL_BK, z = blockIdx.z, splits = gridDim.z;
-        kbeg = z * DL_BK;
-        kstep = splits * DL_BK;
-        nk = z < steps ? (int)((steps - z + splits - 1) / splits) : 0;
+        const uint64_t units = (steps + DL_UNIT - 1) / DL_UNIT;
+        const uint64_t nu = z < units ? (units - z + splits - 1) / splits : 0;
+        uint64_t n_ = nu * DL_UNIT;
+        // The device's last unit may be short; it is this split's last.
+        if (nu && (units - 1 - z) % splits == 0 && steps % DL_UNIT) n_ -= DL_UNIT - steps % DL_UNIT;
+        kbeg = z * DL_UNIT * DL_BK;
+        kstep = splits * DL_UNIT * DL_BK;
+        nk = (int)n_;
     }
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1046,11 +1051,14 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         const bool dl128 = dl_ok(pair, K, N);
         const int BMN = (t128 >= 64 || dl128) ? 128 : 64;
         const uint64_t tiles = BMN == 128 ? t128 : t64;
-        uint64_t splits = (1024 + tiles - 1) / tiles;
+        // The 128-wide tile holds 64 KiB of LDS, two workgroups per CU: one
+        // resident round of them; the other tiles, 1024 workgroups.
+        const uint64_t target = dl128 ? 2 * (uint64_t)device_cus() : 1024;
+        uint64_t splits = (target + tiles - 1) / tiles;
         uint64_t min_splits = (K + KCHUNK - 1) / KCHUNK;
         if (splits < min_splits) splits = min_splits;
         uint64_t kslice = (K + splits - 1) / splits;
-        kslice = (kslice + 127) / 128 * 128;
+        kslice = (kslice + 255) / 256 * 256;
         if (kslice > (uint64_t)KCHUNK) kslice = KCHUNK;
         splits = (K + kslice - 1) / kslice;
         // Grid z is 16 bits; a deeper split folds in registers instead.

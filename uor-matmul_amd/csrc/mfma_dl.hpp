@@ -84,6 +84,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 constexpr int DL_BK = 64;
 constexpr int DL_NSTAGE = 4;
 
+// Steps come in units of DL_UNIT consecutive 64-deep steps (256 bytes of each
+// A row); unit u of a k walk starts kstep bytes after unit u - 1, so kstep =
+// DL_UNIT * DL_BK is the plain contiguous walk.
+constexpr int DL_UNIT = 4;
+__device__ inline uint64_t dl_koff(int t, uint64_t kstep) {
+    return (uint64_t)(t / DL_UNIT) * kstep + (uint64_t)(t % DL_UNIT) * DL_BK;
+}
+
 // One LDS array per workgroup: the A halves of all stages first, then the B
 // halves, so that a stage handle (its A half) reaches its B half at a fixed
 // offset and every fragment read is a lane base plus an immediate offset
@@ -211,22 +219,22 @@ __device__ inline void dl_compute(const char *sa, const char *sb,
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
 }
 
-// The k loop over nk steps of DL_BK, step t at kbeg + t * kstep: each wave's
-// FM x FN 32x32 accumulators, stage handles st0..st3 (A halves; B halves at
-// B_OFF above).  Ends with every load retired; the caller's barrier then frees
-// the stages.
+// The k loop over nk steps of DL_BK, step t at kbeg + dl_koff(t, kstep): each
+// wave's FM x FN 32x32 accumulators, stage handles st0..st3 (A halves; B halves
+// at B_OFF above).  Ends with every load retired; the caller's barrier then
+// frees the stages.
 template <int BM, int BN, int WM, int WN>
 __device__ inline void dl_mainloop(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0,
                                    uint64_t kbeg, int nk, char *st0, char *st1, char *st2,
                                    char *st3, v16i (&acc)[BM / WM / 32][BN / WN / 32],
-                                   uint64_t kstep = DL_BK) {
+                                   uint64_t kstep = DL_UNIT * DL_BK) {
     constexpr int NT = 64 * WM * WN;
     using L = DlLayout<BM, BN>;
     constexpr int LOADS = (BM + BN) * 4 / NT;  // global_load_lds per thread per stage
     static_assert(DL_NSTAGE == 4, "the k loop below is unrolled by four stages");
     if (0 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg, st0);
-    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + kstep, st1);
-    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + 2 * kstep, st2);
+    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + dl_koff(1, kstep), st1);
+    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + dl_koff(2, kstep), st2);
 
     // Step kt reads stage kt % 4 and refills stage (kt + 3) % 4, last read at
     // step kt - 1, which every wave has finished once it passes the barrier.
@@ -238,7 +246,7 @@ __device__ inline void dl_mainloop(const Opnd &A, const Opnd &B, uint64_t m0, ui
         else wait_vm<0>();                                                                     \
         stage_barrier();                                                                       \
         if (kt + DL_NSTAGE - 1 < nk)                                                           \
-            dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + (uint64_t)(kt + DL_NSTAGE - 1) * kstep, NXT); \
+            dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + dl_koff(kt + DL_NSTAGE - 1, kstep), NXT); \
         dl_compute<BM, BN, WM, WN>(CUR, CUR + L::B_OFF, acc);                                \
         if (++kt >= nk) break;                                                                 \
     }
@@ -306,7 +314,7 @@ template <int BM, int BN, int WM, int WN>
 __device__ inline void dl_mainloop_pf(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0,
                                       uint64_t kbeg, int nk, char *st0, char *st1, char *st2,
                                       char *st3, v16i (&acc)[BM / WM / 32][BN / WN / 32],
-                                      uint64_t kstep = DL_BK) {
+                                      uint64_t kstep = DL_UNIT * DL_BK) {
     constexpr int NT = 64 * WM * WN;
     using L = DlLayout<BM, BN>;
     constexpr int LOADS = (BM + BN) * 4 / NT;  // global_load_lds per thread per stage
@@ -315,8 +323,8 @@ __device__ inline void dl_mainloop_pf(const Opnd &A, const Opnd &B, uint64_t m0,
     if (nk <= 0) return;
     DlHalf<BM, BN, WM, WN> f0, f1;
     dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg, st0);
-    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + kstep, st1);
-    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + 2 * kstep, st2);
+    if (1 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + dl_koff(1, kstep), st1);
+    if (2 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + dl_koff(2, kstep), st2);
     {
         const int later = min(2, nk - 1);
         if (later >= 2) wait_vm<2 * LOADS>();
@@ -339,7 +347,7 @@ __device__ inline void dl_mainloop_pf(const Opnd &A, const Opnd &B, uint64_t m0,
         stage_barrier();                                                                       \
         dl_read_half<BM, BN, WM, WN>(CUR, CUR + L::B_OFF, 1, f1);                               \
         dl_mfma_half<BM, BN, WM, WN, 0, NQ / 2>(f0, acc);                                      \
-        if (kt + 3 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + (uint64_t)(kt + 3) * kstep, FREE); \
+        if (kt + 3 < nk) dl_issue<BM, BN, NT>(A, B, m0, n0, kbeg + dl_koff(kt + 3, kstep), FREE); \
         dl_mfma_half<BM, BN, WM, WN, NQ / 2, NQ>(f0, acc);                                     \
         asm volatile("" ::: "memory");                                                         \
         if (kt + 1 < nk) dl_read_half<BM, BN, WM, WN>(NXT, NXT + L::B_OFF, 0, f0);              \
