@@ -299,6 +299,13 @@ __global__ void __launch_bounds__(256) lut4_dot4_pf_kernel(LutArgs L, int book_a
         for (int cc = 0; cc < 4; ++cc) b.cw[cc] = code_chunk<FAST>(L, jf, (uint64_t)(64 * cc + lane) * 16);
     };
     typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+    int slot = 0, pend_sum = 0, pend_row = 0;  // slot: wave-uniform
+    uint64_t pend_col = ~0ull;
+    auto flush = [&]() {
+        if (pend_col < L.n && (uint64_t)pend_row < L.m) lut_finish_any(L, pend_row, pend_col, pend_sum);
+        pend_col = ~0ull;
+        slot = 0;
+    };
     auto compute = [&](uint64_t jc, const Col &b) {
         // The table's address passes through an empty asm each step, so the
         // compiler reads it from LDS per use instead of holding all of it in
@@ -326,11 +333,16 @@ __global__ void __launch_bounds__(256) lut4_dot4_pf_kernel(LutArgs L, int book_a
                 }
             }
         }
+        // Park each (row, column) sum on its own lane; the finish runs for
+        // 64 of them at once (one pass of the output encode per 64 sums, not
+        // one per sum with a single lane active).
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             const int sum = wave_sum(acc[r]);
-            if (lane == r && (uint64_t)r < L.m) lut_finish_any(L, r, jc, sum);
+            if (lane == slot + r) pend_sum = sum, pend_row = r, pend_col = jc;
         }
+        slot += MR;
+        if (slot == 64) flush();
     };
     Col b0, b1, b2;
     uint64_t j = wave;
@@ -349,6 +361,7 @@ __global__ void __launch_bounds__(256) lut4_dot4_pf_kernel(LutArgs L, int book_a
         UOR_LUT_STEP(b2, b1)
     }
 #undef UOR_LUT_STEP
+    flush();
 }
 
 // Resident blocks of a kernel on the whole device (one persistent round).
