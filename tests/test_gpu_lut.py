@@ -66,6 +66,19 @@ def test_epilogue(oracle, uor, dev, out, encode, m):
                  encode=encode)
 
 
+@pytest.mark.parametrize("out", [np.int8, np.int16, np.int32, np.int64])
+@pytest.mark.parametrize("encode", ["nearest", "wrapping"])
+def test_lds_kernel_epilogue(oracle, uor, dev, out, encode):
+    """The LDS-activation kernel's output paths (k % 2048 == 0, 2 <= m <=
+    32): i32 rows in 16-byte stores except the ragged last columns (n = 45),
+    the per-cell finish for the other widths, each with plain, scaled and
+    saturating alpha/beta."""
+    for alpha, beta in [(1, 0), (3, -1), (1 << 40, -(1 << 35))]:
+        route = run_case(oracle, uor, dev, 9, 2048, 45, 8, seed=13, out=out, alpha=alpha,
+                         beta=beta, encode=encode)
+        assert route["kind"] == "lut4_mfma" and route["split_k"] == 1, route
+
+
 def test_deep_rows_fold_exactly(oracle, uor, dev):
     """k past one i32 lane's reach (2^17 weights of |w*a| = 2^14) folds into
     i64: all -128 activations against a codebook of -128 give k * 2^14."""
@@ -130,11 +143,12 @@ def test_mfma16_quarters_at_depth_limit(uor, dev, k):
 
 
 @pytest.mark.parametrize("m,k,n", [(8, 4096, 8192 - 5), (20, 2048, 12288 + 3), (13, 2048, 32768),
-                                   (32, 2048, 28672), (5, 6144, 16 * 256 * 5 + 9), (32, 2048, 64)])
+                                   (32, 2048, 28672), (5, 6144, 16 * 256 * 5 + 9), (32, 2048, 64),
+                                   (2, 8192, 28672), (4, 2048, 1000)])
 def test_tiles_per_cu(uor, dev, m, k, n):
-    """The LDS-activation kernel (4 < m <= 32) with 2, 4, 8, 7, 6 and 1
-    sixteen-column tiles per CU (ragged n, one row block or two, one to three
-    activation chunks), against a decode in torch plus a float64 matmul
+    """The LDS-activation kernel (2 <= m <= 32) with 2, 4, 8, 7, 6, 1, 7 and
+    1 sixteen-column tiles per CU (ragged n, one row block or two, one to
+    three activation chunks), against a decode in torch plus a float64 matmul
     (exact: every sum is an integer below 2^53)."""
     group = 128
     rng = np.random.default_rng(m + k + n)

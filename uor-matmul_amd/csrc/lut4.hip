@@ -739,13 +739,31 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
             asm volatile("" ::: "memory");
         }
         if (active) {
+            // Lane (c, g) holds row 16b + c, columns j0 + 4g .. + 3.  i32 output
+            // with a unit column stride and 16-byte aligned rows leaves in one
+            // 16-byte store per lane (and, with beta != 0, one 16-byte load).
+            const bool vec = L.ob == 4 && L.ccs == 1 && ((uintptr_t)L.c & 15) == 0 && (L.crs & 3) == 0;
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
-                const uint64_t r = 16 * b + c;
+                const uint64_t r = 16 * b + c, col0 = j0 + 4 * g;
+                if (r >= L.m) continue;
+                if (vec && col0 + 4 <= L.n) {
+                    int32_t *cp = (int32_t *)L.c + (int64_t)r * L.crs + (int64_t)col0;
+                    v4i out = acc[b];
+                    if (L.alpha != 1 || L.beta != 0) {
+                        const v4i prior = L.beta != 0 ? *(const v4i *)cp : v4i{};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint64_t col = j0 + 4 * g + i;
-                    if (r < L.m && col < L.n) lut_finish_any(L, r, col, (int64_t)acc[b][i]);
+                        for (int i = 0; i < 4; ++i) {
+                            i128 t = sat_mul((i128)acc[b][i], L.alpha);
+                            if (L.beta != 0) t = (i128)((u128)t + (u128)sat_mul((i128)prior[i], L.beta));
+                            out[i] = (int)encode_int(t, 4, L.mode);
+                        }
+                    }
+                    *(v4i *)cp = out;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (col0 + i < L.n) lut_finish_any(L, r, col0 + i, (int64_t)acc[b][i]);
                 }
             }
         }
@@ -801,13 +819,14 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         route->operand_modes = fast;
     }
     const bool a16 = A.cs == 1 && ((uintptr_t)A.base % 16 == 0) && (A.rs % 16 == 0 || m == 1);
-    // 4 < m <= 32, whole 2048-weight blocks, k <= 65536 (each wave's i32 sum
+    // 2 <= m <= 32, whole 2048-weight blocks, k <= 65536 (each wave's i32 sum
     // over the whole depth is exact), 16-byte aligned code rows (all below
     // 2^31 bytes) and activation rows: one workgroup per CU with the
     // activations in LDS.  Its waves must cover a chunk's m*KC/1024 pieces at
-    // one per wave per step: W >= m/8.  (For m <= 4 the dot4 kernels below
-    // are faster: 28 us against 33 us at m = 1, k = 8192, n = 28672.)
-    if (m > 4 && m <= 32 && k % 2048 == 0 && k <= 65536 && code_fast && a16 && n * (k / 2) < (1ull << 31) &&
+    // one per wave per step: W >= m/8.  (At k = 8192, n = 28672 it takes
+    // 29.8 us for every m from 1 to 8; the dot4 kernel below takes 25.4 us at
+    // m = 1 and 30.2, 37.7, 39.1 us at m = 2, 3, 4.)
+    if (m >= 2 && m <= 32 && k % 2048 == 0 && k <= 65536 && code_fast && a16 && n * (k / 2) < (1ull << 31) &&
         lut_variant() == 1) {
         const uint64_t ntiles = (n + 15) / 16;
         const uint64_t cus = (uint64_t)device_cus_lut();
