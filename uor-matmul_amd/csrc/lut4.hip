@@ -563,41 +563,73 @@ lut4_mfma16_kernel(LutArgs L, int book_aligned, uint64_t qsteps) {
     }
 }
 
-// ------------------------ m <= 32, one workgroup per CU, activations in LDS
+// ------------------------ 2 <= m <= 32, one workgroup per CU, activations in LDS
 //
 // The workgroup owns T consecutive 16-column tiles (T = tiles per CU), one
-// wave per tile over the whole depth (more than 16 tiles: rounds of W), so no
-// partial sums cross waves.  Per 128-weight step, lane (c = l%16, g = l/16)
+// wave per tile over the whole depth (more tiles than waves: rounds of W), so
+// no partial sums cross waves.  Per 128-weight step, lane (c = l%16, g = l/16)
 // loads the 16 code bytes of column j0+c covering weights [32g, 32g+32) of
-// the step (a column's 64 bytes per step are contiguous) and decodes them
-// into two v_mfma_i32_16x16x64_i8 A operands, in the decode's own order:
-// per 8 weights the even ones, then the odd ones.  The activations are what
-// the waves share: they pass through LDS in chunks of KC weights (16*MB rows
-// x KC bytes, double-buffered), read from global memory once per workgroup in
-// coalesced 1 KiB pieces (one row's 1024 consecutive weights) and stored in
-// that same even/odd order, so each B operand is one ds_read_b128 and needs
-// no rearranging.  Chunk c+1's pieces are loaded during chunk c, one per wave
-// per step, and written PD = 8 steps later; a barrier closes each chunk.
-// Codes are loaded CR = 16 steps ahead through a buffer resource, so the
-// loads past the last step read zeros instead of leaving the buffer.  (Loads
-// retire in order, so a piece's write waits for every code load issued before
-// it: the write delay bounds how far ahead the codes really are.)
+// the step (a column's 64 bytes per step are contiguous) and decodes them, in
+// natural weight order, into two v_mfma_i32_16x16x64_i8 A operands.  The
+// activations are what the waves share: they pass through LDS in chunks of
+// KC weights (16*MB rows x KC bytes, double-buffered), each 1 KiB piece (one
+// row's 1024 consecutive weights) copied from global memory straight into LDS
+// by global_load_lds_dwordx4, so each B operand is one ds_read_b128.  Chunk
+// c+1's pieces are issued in the first steps of chunk c, one per wave per
+// step; each wave waits for its own pieces before the barrier that closes
+// the chunk, which otherwise leaves the code loads in flight.  Codes are
+// loaded CR = 16 steps ahead through a buffer resource, so the loads past the
+// last step read zeros instead of leaving the buffer.
 //
 // LDS layout of a chunk buffer: row r, 16-byte chunk x at r*KC + 16*(x ^ (r & 15)),
-// so the 16 rows a B-operand read touches sit on distinct banks.  Everything
-// about a piece except the lane's 16 bytes is wave-uniform (scalar); pieces
-// outside the set read a valid place and write a dummy slot, so every step
-// has the same instructions.
+// so the 16 rows a B-operand read touches sit on distinct banks.  A piece
+// lands contiguously (lane L at +16L), so lane L fetches the chunk whose
+// place that is: x = 64p + (L ^ (r & 15)).
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// Lane L's 16 bytes at g land at LDS byte lds + 16*L.  M0 is reserved by the
+// compiler, which warns on the clobber; the kernel that calls this makes no
+// other use of M0.
+__device__ inline void lut_dma16(const int8_t *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(min(n, 15)), expcnt and lgkmcnt unconstrained (n is
+// wave-uniform; the immediate needs a branch per value).
+__device__ inline void lut_wait_vm(int n) {
+#define UOR_VM(N) case N: __builtin_amdgcn_s_waitcnt((N) | (0x7 << 4) | (0xF << 8)); break;
+    switch (n < 15 ? (n < 0 ? 0 : n) : 15) {
+        UOR_VM(0) UOR_VM(1) UOR_VM(2) UOR_VM(3) UOR_VM(4) UOR_VM(5) UOR_VM(6) UOR_VM(7)
+        UOR_VM(8) UOR_VM(9) UOR_VM(10) UOR_VM(11) UOR_VM(12) UOR_VM(13) UOR_VM(14)
+        default: __builtin_amdgcn_s_waitcnt(15 | (0x7 << 4) | (0xF << 8)); break;
+    }
+#undef UOR_VM
+}
+
+// decode8 in natural order: lo = [w0 w1 w2 w3], hi = [w4 w5 w6 w7].
+__device__ inline void decode8n(uint32_t w, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3,
+                                uint32_t m4, uint32_t id, uint32_t &lo, uint32_t &hi) {
+    uint32_t e, o;
+    decode8(w, q0, q1, q2, q3, m4, id, e, o);
+    lo = perm(o, e, 0x05010400u);
+    hi = perm(o, e, 0x07030602u);
+}
+
 template <int MB>
 __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_aligned, uint32_t tpw) {
-    constexpr int CR = 16, PD = 8;  // code ring (steps ahead), piece write delay
+    constexpr int CR = 16;         // code ring (steps ahead)
     constexpr int ROWS = 16 * MB;
     constexpr int KC = 4096 / MB;  // weights per chunk
     constexpr int S = KC / 128;    // steps per chunk
     constexpr int PPR = KC / 1024; // pieces per row per chunk
     constexpr int CB = ROWS * KC;  // bytes per chunk buffer (64 KiB)
     static_assert(S % CR == 0 && PPR >= 1, "chunk shape");
-    __shared__ __attribute__((aligned(16))) int8_t abuf[2 * CB + 1024];
+    __shared__ __attribute__((aligned(16))) int8_t abuf[2 * CB];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = blockDim.x >> 6;
@@ -605,31 +637,21 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
     const uint64_t nsteps = L.k / 128, nchunks = (L.k + KC - 1) / KC;
     const uint64_t ntiles = (L.n + 15) / 16;
     const uint64_t t0 = (uint64_t)blockIdx.x * tpw, t1 = min(t0 + tpw, ntiles);
-    const int P = (int)L.m * PPR;  // pieces per full chunk
+    const int P = (int)L.m * PPR;  // pieces per chunk
     const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)abuf;
-    typedef __attribute__((address_space(3))) v4i lds_v4i;
     typedef __attribute__((address_space(3))) const v4i lds_v4i_c;
 
-    // Piece q of chunk ch (wave-uniform): row q / PPR, weights ch*KC +
-    // (q % PPR)*1024 + 16*lane ..; lane L's 16-byte chunk x = (q % PPR)*64 + L
-    // lands at row*KC + 16*(x ^ (row & 15)) = ... + 16*(L ^ (row & 15)).
-    auto piece_load = [&](uint64_t ch, int q, uint32_t &dst) -> v4i {
+    // Piece q of chunk ch into chunk buffer buf (all wave-uniform but the
+    // lane's source): row q / PPR, weights ch*KC + (q % PPR)*1024 ...; false
+    // (and nothing issued) past the chunk's last piece or past k.
+    auto piece_dma = [&](uint64_t ch, int q, int buf) -> bool {
         const int row = q / PPR, part = q % PPR;
         const uint64_t kb = ch * KC + (uint64_t)part * 1024;
-        const bool ok = q < P && ch < nchunks && kb < L.k;
-        const int8_t *src = ok ? L.a + (int64_t)row * L.ars + (int64_t)kb : L.a;
-        dst = ok ? (uint32_t)(row * KC + part * 1024) + 16u * (uint32_t)(lane ^ (row & 15)) : (uint32_t)(2 * CB) + 16u * lane;
-        return *(const v4i *)(src + 16 * lane);
-    };
-    // Stored in the decode's order: per 8 weights the even ones, then the odd
-    // ones.  (The rearranging happens here, at the store, so a load's first
-    // use is the store that comes PD steps later.)
-    auto piece_store = [&](int buf, uint32_t dst, const v4i &x) {
-        const uint32_t off = dst < (uint32_t)(2 * CB) ? dst + (uint32_t)(buf * CB) : dst;
-        const v4i v = v4i{(int)perm((uint32_t)x[1], (uint32_t)x[0], 0x06040200u), (int)perm((uint32_t)x[1], (uint32_t)x[0], 0x07050301u),
-                          (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x06040200u), (int)perm((uint32_t)x[3], (uint32_t)x[2], 0x07050301u)};
-        *(lds_v4i *)(uintptr_t)(lds0 + off) = v;
+        if (q >= P || kb >= L.k) return false;
+        const int8_t *src = L.a + (int64_t)row * L.ars + (int64_t)kb + 16 * (lane ^ (row & 15));
+        lut_dma16(src, lds0 + (uint32_t)(buf * CB + row * KC + part * 1024));
+        return true;
     };
     // B-operand read offsets: weights 128*sl + 32g + [0,16) are chunk
     // x = 8sl + 2g, at 256*(sl >> 1) + 16*((8*(sl & 1) + 2g) ^ c) in the row
@@ -654,44 +676,34 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
         load_book(L, jl, book_aligned, q0, q1, q2, q3);
         const uint32_t cvo = (uint32_t)(jl * L.half) + 16u * g;  // this lane's code offset at step 0
 
-        // The first CR steps of codes, then chunk 0's pieces in batches of
-        // eight per wave, each batch's loads in flight together.
+        // Chunk 0's pieces, then the first CR steps of codes; waiting until
+        // at most CR loads are left retires every piece (loads retire in
+        // order).
+        for (int q = wave; q < P; q += W) piece_dma(0, q, 0);
         v4i ring[CR];
 #pragma unroll
         for (int u = 0; u < CR; ++u) ring[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(crs, cvo, u * 64, 0));
-        for (int qb = wave; qb < P; qb += 8 * W) {
-            v4i pv[8];
-            uint32_t pd[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) pv[i] = piece_load(0, qb + i * W, pd[i]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) piece_store(0, pd[i], pv[i]);
-        }
-        __syncthreads();
+        lut_wait_vm(CR);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
 
         v4i acc[MB];
 #pragma unroll
         for (int b = 0; b < MB; ++b) acc[b] = v4i{};
-        v4i pr[PD];
-        uint32_t pdst[PD];
-#pragma unroll
-        for (int t = 0; t < PD; ++t) pr[t] = v4i{}, pdst[t] = (uint32_t)(2 * CB);
-        static_assert(S % PD == 0, "the chunk's last PD steps sit in ring order");
         for (uint64_t ch = 0; ch < nchunks; ++ch) {
             const int cur = (int)(ch & 1), nxt = cur ^ 1;
             const bool more = ch + 1 < nchunks;
             const uint64_t sbeg = ch * S, send = min(nsteps, sbeg + S);
+            int last = -1;  // the step of this wave's last piece copy in the chunk
             for (uint64_t s8 = sbeg; s8 < send; s8 += CR) {
                 const uint32_t cb_off = (uint32_t)(cur * CB) + 128u * (uint32_t)(s8 - sbeg);
 #pragma unroll
                 for (int u = 0; u < CR; ++u) {
                     const uint64_t st = s8 + u;
                     const int sl = (int)(s8 - sbeg) + u;
-                    // The next chunk's pieces: write the one loaded PD steps
-                    // ago (in this chunk), load one.  Steps past the last
-                    // piece load and store nothing (wave-uniform branches).
-                    if (more && sl >= PD && (sl - PD) * W + wave < P) piece_store(nxt, pdst[u % PD], pr[u % PD]);
-                    if (more && sl * W + wave < P) pr[u % PD] = piece_load(ch + 1, sl * W + wave, pdst[u % PD]);
+                    // One of the next chunk's pieces (wave-uniform branch).
+                    if (more && sl * W + wave < P && piece_dma(ch + 1, sl * W + wave, nxt)) last = sl;
                     // Codes of step st.
                     const v4i cw = ring[u];
                     // B operands from LDS.
@@ -702,13 +714,11 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
                         x0[b] = *(lds_v4i_c *)(uintptr_t)(boff[u & 1][0] + ro);
                         x1[b] = *(lds_v4i_c *)(uintptr_t)(boff[u & 1][1] + ro);
                     }
-                    uint32_t e[4], o[4];
-                    decode8((uint32_t)cw[0], q0, q1, q2, q3, m4, id, e[0], o[0]);
-                    decode8((uint32_t)cw[1], q0, q1, q2, q3, m4, id, e[1], o[1]);
-                    decode8((uint32_t)cw[2], q0, q1, q2, q3, m4, id, e[2], o[2]);
-                    decode8((uint32_t)cw[3], q0, q1, q2, q3, m4, id, e[3], o[3]);
-                    const v4i w01 = v4i{(int)e[0], (int)o[0], (int)e[1], (int)o[1]};
-                    const v4i w23 = v4i{(int)e[2], (int)o[2], (int)e[3], (int)o[3]};
+                    uint32_t lo[4], hi[4];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) decode8n((uint32_t)cw[d], q0, q1, q2, q3, m4, id, lo[d], hi[d]);
+                    const v4i w01 = v4i{(int)lo[0], (int)hi[0], (int)lo[1], (int)hi[1]};
+                    const v4i w23 = v4i{(int)lo[2], (int)hi[2], (int)lo[3], (int)hi[3]};
                     // The load of step st + CR goes into the ring slot just
                     // read, after the decode: issued earlier, it would need a
                     // second register set and copies (each waiting for its
@@ -723,17 +733,11 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
                     }
                 }
             }
-            // The last PD pieces of the next chunk (the chunk's step count is
-            // a multiple of CR, so they sit in ring order), then the barrier
-            // that closes this chunk (its reads done, the next one written).
-            // The barrier waits for this wave's LDS writes only: the code
-            // loads stay in flight across it.
-            if (more) {
-#pragma unroll
-                for (int t = 0; t < PD; ++t)
-                    if ((S - PD + t) * W + wave < P) piece_store(nxt, pdst[t], pr[t]);
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            // Close the chunk: this wave's piece copies have landed once at
+            // most the code loads issued after the last of them are left
+            // (one per step from that step on); then the barrier (every
+            // wave's reads of this chunk done, the next one written).
+            if (last >= 0) lut_wait_vm((int)(send - sbeg) - last);
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
