@@ -362,3 +362,44 @@ def test_splitk_interleaved_steps(uor, dev, m, k, n):
     S = (a.view(m, k).double() @ b.view(k, n).double()).cpu().numpy().astype(np.int64)
     want = 3 * S - c0.reshape(m, n)
     assert np.array_equal(c.cpu().numpy().reshape(m, n), want)
+
+
+@pytest.mark.parametrize("m,k,n", [(40, (1 << 20) + 768, 144), (100, (1 << 20) + 256, 16)])
+def test_splitk_narrow_tile_far_rows(uor, dev, m, k, n):
+    """A rows 1 MiB or more apart take the 32x128 split-K tile (a CU touches
+    32 row pages, not 128): ragged m and n, stage counts not a multiple of
+    the split count.  Random i8 operands, i64 output with alpha = 3,
+    beta = -1; expected values from an exact float64 product."""
+    g = torch.Generator(device=dev).manual_seed(m + n)
+    a = torch.randint(-128, 128, (m * k,), dtype=torch.int8, device=dev, generator=g)
+    b = torch.randint(-128, 128, (k * n,), dtype=torch.int8, device=dev, generator=g)
+    c0 = torch.randint(-(1 << 40), 1 << 40, (m * n,), dtype=torch.int64, device=dev, generator=g)
+    c = c0.clone()
+    scratch = torch.empty(uor.suggested_scratch_i8(m, k, n), dtype=torch.uint8, device=dev)
+    st, route = uor.gemm_i8(a, (m, k), (k, 1), b, (k, n), (n, 1), c, (m, n), (n, 1), out="i64",
+                            alpha=3, beta=-1, scratch=scratch)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_splitk" and route["tile_m"] == 32, route
+    S = a.view(m, k).double() @ b.view(k, n).double()
+    want = 3 * S.cpu().numpy().astype(np.int64) - c0.cpu().numpy().reshape(m, n)
+    assert np.array_equal(c.cpu().numpy().reshape(m, n), want)
+
+
+def test_splitk_narrow_tile_folds_segments(uor, dev):
+    """The 32x128 split-K tile folds each split's i32 lanes into i64 every
+    256 stages (65 536 terms): at k = 2^24 + 512 one tile takes one split per
+    CU, and each split sums 256 or 257 stages (a fold, then for two of them
+    one stage more).  Random operands against float64 (|sum| <= 2^38 <
+    2^53)."""
+    m, k, n = 32, (1 << 24) + 512, 16
+    g = torch.Generator(device=dev).manual_seed(7)
+    a = torch.randint(-128, 128, (m * k,), dtype=torch.int8, device=dev, generator=g)
+    b = torch.randint(-128, 128, (k * n,), dtype=torch.int8, device=dev, generator=g)
+    c = torch.zeros(m * n, dtype=torch.int64, device=dev)
+    scratch = torch.empty(uor.suggested_scratch_i8(m, k, n), dtype=torch.uint8, device=dev)
+    st, route = uor.gemm_i8(a, (m, k), (k, 1), b, (k, n), (n, 1), c, (m, n), (n, 1), out="i64",
+                            scratch=scratch)
+    torch.cuda.synchronize()
+    assert st == 0 and route["tile_m"] == 32, route
+    S = (a.view(m, k).double() @ b.view(k, n).double()).cpu().numpy().astype(np.int64)
+    assert np.array_equal(c.cpu().numpy().reshape(m, n), S)

@@ -861,6 +861,131 @@ __global__ void __launch_bounds__(256) zero_i64_kernel(long long *p, uint64_t co
     if (idx < count) p[idx] = 0;
 }
 
+// ------------------------------------------------- deep, narrow-tile split-K --
+//
+// For A rows far apart in memory (every row its own page, as in the deep
+// shapes m = n = 128, k = 2^24), a 128-row tile touches 128 pages per step and
+// the address translation, not HBM, sets the pace.  This tile is 32 rows x 128
+// columns: a CU touches 32 row pages of A (plus B's one), and the four tiles
+// that share B's k-range run on one XCD at the same time (ids 8 apart), so B
+// comes from HBM once and from L2 for the others.  Per 256-deep stage: A is
+// 32 rows x 256 bytes (8 KiB), B 256 k-rows x 128 bytes (32 KiB), both by
+// global_load_lds_dwordx4; three stages in LDS (120 KiB), two in flight.
+// Wave w owns columns [32w, 32w + 32): one 32x32 accumulator, eight
+// v_mfma_i32_32x32x32_i8 per stage.  Split z sums the stages z, z + splits,
+// ... (neighbouring splits read neighbouring 256-byte pieces of every row) and
+// folds its i32 lanes into i64 every 256 stages (65 536 terms, |sum| < 2^30),
+// then adds its i64 partial into the workspace.
+//
+// LDS: A row r (0..31), 16-byte chunk x (0..15) at r*256 + 16*(x ^ (r & 15));
+// B as the 128-wide direct-to-LDS tile's B half (k*128 + 16*(x ^ swz(k))).
+constexpr int DP_BM = 32, DP_BN = 128, DP_BK = 256;
+constexpr int DP_A = DP_BM * DP_BK, DP_B = DP_BK * DP_BN, DP_STAGE = DP_A + DP_B;
+constexpr int DP_LOADS = DP_STAGE / 1024 / 4;  // global_load_lds per wave per stage (10)
+constexpr int DP_FOLD = 256;                   // stages per exact i32 segment
+
+__device__ inline int dp_bswz(int k) { return (2 * (k & 7)) & (DP_BN / 16 - 1); }
+
+__device__ inline void dp_issue(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t k0,
+                                char *stage) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // A: 512 chunks, slot s = row * 16 + physical chunk p; p holds chunk p ^ (row & 15).
+#pragma unroll
+    for (int i = 0; i < DP_A / 1024 / 4; ++i) {
+        const int base = (wave * (DP_A / 1024 / 4) + i) * 64, slot = base + lane;
+        const int row = slot >> 4, x = (slot & 15) ^ (row & 15);
+        uint64_t gr = m0 + row;
+        if (gr >= A.mn) gr = A.mn - 1;  // rows past m are computed and discarded
+        lds_dma16(A.base + (int64_t)gr * A.s_mn + (int64_t)(k0 + 16 * x), stage + base * 16);
+    }
+    // B: 2048 chunks, slot s = k * 8 + physical chunk p; p holds chunk p ^ swz(k).
+    char *bst = stage + DP_A;
+#pragma unroll
+    for (int i = 0; i < DP_B / 1024 / 4; ++i) {
+        const int base = (wave * (DP_B / 1024 / 4) + i) * 64, slot = base + lane;
+        const int k = slot >> 3, x = (slot & 7) ^ dp_bswz(k);
+        uint64_t gn = n0 + 16 * x;
+        if (gn >= B.mn) gn = 0;  // columns past n are computed and discarded
+        lds_dma16(B.base + (int64_t)(k0 + k) * B.s_k + (int64_t)gn, bst + base * 16);
+    }
+}
+
+__device__ inline void dp_compute(const char *st, v16i &acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int half = lane >> 5, l32 = lane & 31, grp = lane >> 4, t16 = lane & 15;
+    const char *sb = st + DP_A;
+    v4i af[DP_BK / 32], bf[DP_BK / 32];
+#pragma unroll
+    for (int ks = 0; ks < DP_BK / 32; ++ks) {
+        const int x = 2 * ks + half;
+        af[ks] = *(const v4i *)(st + l32 * DP_BK + 16 * (x ^ (l32 & 15)));
+        const int nb = 32 * wave + 16 * (grp & 1) + 8 * (t16 & 1);
+        const int k = 32 * ks + 16 * (grp >> 1) + (t16 >> 1);
+        v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i *)(sb + k * DP_BN + 16 * ((nb >> 4) ^ dp_bswz(k)) + (nb & 8)));
+        v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i *)(sb + (k + 8) * DP_BN + 16 * ((nb >> 4) ^ dp_bswz(k + 8)) + (nb & 8)));
+        bf[ks] = v4i{lo[0], lo[1], hi[0], hi[1]};
+    }
+#pragma unroll
+    for (int ks = 0; ks < DP_BK / 32; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks], bf[ks], acc, 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256, 1)
+gemm_i8_deep_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn, int splits) {
+    __shared__ __attribute__((aligned(16))) char lds[3 * DP_STAGE];
+    char *const s0 = lds, *const s1 = lds + DP_STAGE, *const s2 = lds + 2 * DP_STAGE;
+    // id -> (tile, split): ids on one XCD (id % 8) take consecutive tiles of
+    // one split, so the tiles sharing B's k-range meet in one L2.
+    const int id = blockIdx.x, xcd = id % 8, slot = id / 8, tiles = gm * gn;
+    const int tile = slot % tiles, z = (slot / tiles) * 8 + xcd;
+    const uint64_t m0 = (uint64_t)(tile % gm) * DP_BM, n0 = (uint64_t)(tile / gm) * DP_BN;
+    const uint64_t stages = K / DP_BK;
+    const int nk = (uint64_t)z < stages ? (int)((stages - z + splits - 1) / splits) : 0;
+    const uint64_t kbeg = (uint64_t)z * DP_BK, kstep = (uint64_t)splits * DP_BK;
+
+    v16i acc = v16i{};
+    long long wide[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wide[r] = 0;
+    if (0 < nk) dp_issue(A, B, m0, n0, kbeg, s0);
+    if (1 < nk) dp_issue(A, B, m0, n0, kbeg + kstep, s1);
+    // Stage t sits in buffer t % 3; step t refills buffer (t + 2) % 3, last
+    // read at step t - 1, which every wave has finished once it passes the
+    // barrier.
+#define UOR_DP_STEP(CUR, NXT)                                                         \
+    {                                                                                 \
+        if (kt + 1 < nk) wait_vm<DP_LOADS>();                                         \
+        else wait_vm<0>();                                                            \
+        stage_barrier();                                                              \
+        if (kt + 2 < nk) dp_issue(A, B, m0, n0, kbeg + (uint64_t)(kt + 2) * kstep, NXT); \
+        dp_compute(CUR, acc);                                                         \
+        if ((kt + 1) % DP_FOLD == 0) {                                                \
+            _Pragma("unroll") for (int r = 0; r < 16; ++r) wide[r] += acc[r];         \
+            acc = v16i{};                                                             \
+        }                                                                             \
+        if (++kt >= nk) break;                                                        \
+    }
+    for (int kt = 0; kt < nk;) {
+        UOR_DP_STEP(s0, s2)
+        UOR_DP_STEP(s1, s0)
+        UOR_DP_STEP(s2, s1)
+    }
+#undef UOR_DP_STEP
+    wait_vm<0>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int half = lane >> 5, l32 = lane & 31;
+    const uint64_t col = n0 + 32 * wave + l32;
+    if (col >= B.mn) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint64_t row = m0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const long long v = wide[r] + acc[r];
+        if (row < A.mn && v != 0)
+            atomicAdd((unsigned long long *)(out.work + row * B.mn + col), (unsigned long long)v);
+    }
+}
+
 // ------------------------------------------------------------------- host --
 
 template <int BM, int BN, int BK, int MA, int MB, int EPI, bool FAST>
@@ -1049,6 +1174,36 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         // streams whole 128-byte B rows, which matters most for the deep,
         // HBM-bound shapes), else 128 or 64 by the tile count.
         const bool dl128 = dl_ok(pair, K, N);
+        // A rows at least 1 MiB apart (each its own page) and few output
+        // tiles: the 32x128 tile, one resident workgroup per CU, each split
+        // folding its own i32 segments (no depth limit per split).
+        if (pair == 0 && K % DP_BK == 0 && N % 16 == 0 && A.s_mn >= (1 << 20) && t128 <= 64) {
+            const uint64_t gm = (M + DP_BM - 1) / DP_BM, gn = (N + DP_BN - 1) / DP_BN, tiles = gm * gn;
+            const uint64_t cus = (uint64_t)device_cus();
+            uint64_t splits = (cus + tiles - 1) / tiles;
+            splits = (splits + 7) / 8 * 8;
+            out.work = (long long *)scratch;
+            const uint64_t cells = M * N;
+            hipLaunchKernelGGL(zero_i64_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s,
+                               out.work, cells);
+            UOR_HIP(hipGetLastError());
+            hipLaunchKernelGGL(gemm_i8_deep_kernel, dim3((unsigned)(tiles * splits)), dim3(256), 0, s, A, B, out,
+                               K, (int)gm, (int)gn, (int)splits);
+            UOR_HIP(hipGetLastError());
+            hipLaunchKernelGGL((finish_kernel<FAST, false>), dim3((unsigned)((cells + 255) / 256)), dim3(256), 0,
+                               s, out, M, N);
+            UOR_HIP(hipGetLastError());
+            if (route) {
+                route->kind = UOR_ROUTE_MFMA_SPLITK;
+                route->tile_m = DP_BM;
+                route->tile_n = DP_BN;
+                route->tile_k = DP_BK;
+                route->split_k = (int)splits;
+                route->launches = 3;
+                route->scratch_used = splitk_bytes(M, N);
+            }
+            return UOR_OK;
+        }
         const int BMN = (t128 >= 64 || dl128) ? 128 : 64;
         const uint64_t tiles = BMN == 128 ? t128 : t64;
         // The 128-wide tile holds 64 KiB of LDS, two workgroups per CU: one
