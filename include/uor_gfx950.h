@@ -88,6 +88,8 @@ typedef struct uor_view {
 #define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
 #define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
 #define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */
+#define UOR_ROUTE_INT_CRT 40      /* i16/i32/i64 elements: int8 residue MFMA + CRT */
+#define UOR_ROUTE_INT_DIRECT 41   /* i16/i32/i64 elements: per-cell exact loop */
 typedef struct uor_route {
     int32_t kind;
     int32_t tile_m, tile_n, tile_k;
@@ -148,6 +150,26 @@ int uor_gfx950_slice_gemm_i8(uint64_t m, uint64_t k, uint64_t n,
  * reference's figure sizes CPU panels, which this route does not use.
  */
 uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n);
+
+/*
+ * The view API at E = i16, i32, i64 (elem_bytes 2, 4, 8; 1 forwards to
+ * uor_gfx950_gemm_i8): the reference's Kernelized integer families
+ * (crates/uor-matmul-gemm/src/kernel.rs:132-399, gemm_auto kernel.rs:523),
+ * AccOf = i128 for i16/i32 and Limbs<3> for i64 (alphabet.rs:559-616,
+ * acc.rs:215), Linear::finish and encode_i128_into / impl_encode_from_limbs
+ * (epilogue.rs:67-95, acc.rs:128-150, 405-442).  The sum is exact at any
+ * depth.  i64 elements: alpha = 1 and beta = 0 only (other scalars return
+ * UOR_INVALID_ARGUMENT).  a, b: views of elem_bytes-byte integers; c: a view
+ * of `out_type` elements.  With an offer of uor_gfx950_suggested_scratch_int
+ * bytes the int8 residue route runs; with none, a per-cell loop.
+ */
+int uor_gfx950_gemm_int(int elem_bytes, const uor_view *a, const uor_view *b,
+                        const uor_view *c, int out_type, int64_t alpha, int64_t beta,
+                        int encode, void *scratch, uint64_t scratch_bytes, void *stream,
+                        uor_route *route);
+
+/* The offer that lets gemm_int take the residue route at this shape. */
+uint64_t uor_gfx950_suggested_scratch_int(int elem_bytes, uint64_t m, uint64_t k, uint64_t n);
 
 /* ============================================ 4-bit table-lookup GEMM */
 

@@ -795,6 +795,7 @@ struct ResOut {
     uint64_t kp, np;
     int sa_max, sb_max;
     const CrtHdr *h;
+    int accumulate;  // 1: add the planes' residues to y's (a later k chunk)
 };
 
 // One (diagonal, modulus) per grid (y, z): the exact i32 sum over the
@@ -850,6 +851,10 @@ residue_gemm_kernel(uint64_t m, uint64_t n, int gm, int gn, ResOut R) {
                 } else {
                     q = v - p * (int)floor((double)v * invp);
                     if (q < 0) q += p;
+                    if (q >= p) q -= p;
+                }
+                if (R.accumulate) {
+                    q += y[row * n + col];
                     if (q >= p) q -= p;
                 }
                 y[row * n + col] = (uint8_t)q;
@@ -1271,6 +1276,349 @@ static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, 
     return hipGetLastError();
 }
 
+// ------------------------------------------------ integer element route --
+//
+// The view API at E = i16, i32, i64: the reference's Kernelized families
+// (crates/uor-matmul-gemm/src/kernel.rs:132-399; AccOf = i128 for i16 and
+// i32, Limbs<3> for i64: alphabet.rs:559-616, acc.rs:215), on the residue
+// pipeline above.  An element is its own integer (line lo = 0, width = the
+// bit length of the line's largest magnitude, at most 64), so the plan is
+// never sliced and |X_ij| < 2^B with B <= 128 + log2 k takes at most 28
+// moduli.  Depth beyond 2^17 (the i32 reach of one residue GEMM) runs in
+// chunks whose residues add mod p.  Cells the plan cannot cover, and every
+// cell when the offer holds no planes, take the per-cell loop.
+
+struct IArgs {
+    const char *a;  // element (0,0)
+    int64_t ars, acs;
+    const char *b;
+    int64_t brs, bcs;
+    char *c;
+    int64_t crs, ccs;
+    uint64_t m, k, n;
+    int64_t alpha, beta;
+    int mode;
+    int ob;     // output bytes
+    int limbs;  // 1: i64 elements (Limbs<3> accumulator; alpha = 1, beta = 0)
+};
+
+template <int EB>
+__device__ inline int64_t load_ielem(const char *base, int64_t idx) {
+    if constexpr (EB == 2) return ((const int16_t *)base)[idx];
+    else if constexpr (EB == 4) return ((const int32_t *)base)[idx];
+    else return ((const int64_t *)base)[idx];
+}
+
+__device__ inline uint64_t mag64(int64_t v) { return v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v; }
+
+// A 192-bit two's complement integer (Limbs<3>).
+struct W192 {
+    uint64_t w[3];
+};
+
+__device__ inline void w192_add(W192 &x, i128 v) {
+    const u128 lo = (u128)x.w[0] + (uint64_t)(u128)v;
+    x.w[0] = (uint64_t)lo;
+    const u128 mid = (u128)x.w[1] + (uint64_t)((u128)v >> 64) + (uint64_t)(lo >> 64);
+    x.w[1] = (uint64_t)mid;
+    x.w[2] = x.w[2] + (v < 0 ? ~(uint64_t)0 : 0) + (uint64_t)(mid >> 64);
+}
+
+// Line statistics of integer lines: lo = 0, width = bit length of the
+// largest magnitude, l1 an upper bound of log2 of the sum of magnitudes.
+template <int EB, bool CONTIG>
+__global__ void __launch_bounds__(256) int_line_stats_kernel(const char *base, int64_t s_line,
+                                                             int64_t s_elem, uint64_t lines,
+                                                             uint64_t len, LineStat *out) {
+    constexpr int LPB = CONTIG ? 1 : 16;  // lines per block
+    constexpr int TPL = 256 / LPB;        // threads per line
+    __shared__ int s_hi[256];
+    __shared__ double s_sum[256];
+    const int t = threadIdx.x;
+    const int tl = CONTIG ? 0 : (t & 15), te = CONTIG ? t : (t >> 4);
+    const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
+    const bool live = line < lines;
+    int hi = 0;
+    if (live)
+        for (uint64_t e = te; e < len; e += TPL) {
+            const uint64_t v = mag64(load_ielem<EB>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
+            if (v) hi = max(hi, bitlen64(v));
+        }
+    s_hi[t] = hi;
+    __syncthreads();
+    for (int w = TPL / 2; w >= 1; w >>= 1) {
+        if (te < w) s_hi[t] = max(s_hi[t], s_hi[CONTIG ? t + w : t + 16 * w]);
+        __syncthreads();
+    }
+    hi = s_hi[tl];
+    double sum = 0;
+    if (live && hi > 0)
+        for (uint64_t e = te; e < len; e += TPL) {
+            const uint64_t v = mag64(load_ielem<EB>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
+            if (v) sum += ldexp((double)v, -hi);
+        }
+    s_sum[t] = sum;
+    __syncthreads();
+    for (int w = TPL / 2; w >= 1; w >>= 1) {
+        if (te < w) s_sum[t] += s_sum[CONTIG ? t + w : t + 16 * w];
+        __syncthreads();
+    }
+    if (te == 0 && live) {
+        LineStat st;
+        st.lo = 0;
+        if (hi == 0) {
+            st.width = 0;
+            st.l1 = -1e30f;
+            st.flags = LS_EMPTY;
+        } else {
+            st.width = hi;
+            // Each term is rounded to 53 bits (relative 2^-53) and the sum
+            // adds at most 2^-30 relative for any reachable length.
+            const double sm = s_sum[tl] * (1.0 + 0x1p-28);
+            st.l1 = (float)(log2(sm) + (double)hi + 1e-6);
+            st.flags = 0;
+        }
+        out[line] = st;
+    }
+}
+
+// x mod p_l for x < 2^32.
+__device__ inline uint32_t umod_p(uint32_t x, int l) {
+    const int64_t p = crt_mod[l];
+    const int64_t q = (int64_t)floor((double)x * crt_invp[l]);
+    int64_t r = (int64_t)x - q * p;
+    if (r < 0) r += p;
+    if (r >= p) r -= p;
+    return (uint32_t)r;
+}
+
+// The balanced int8 residue of v modulo crt_mod[l].
+__device__ inline int int_residue(int64_t v, int l) {
+    const uint64_t a = mag64(v);
+    int r;
+    if (l == 0) {
+        r = (int)(a & 255);
+    } else {
+        const uint32_t p32 = umod_p(umod_p(65536u, l) * umod_p(65536u, l), l);  // 2^32 mod p
+        const uint32_t rh = umod_p((uint32_t)(a >> 32), l), rl = umod_p((uint32_t)a, l);
+        r = (int)umod_p(rh * p32 + rl, l);
+    }
+    const int p = crt_mod[l];
+    int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
+    if (v < 0) b = -b;
+    if (b == 128) b = -128;  // p = 256: 128 and -128 are one residue
+    return b;
+}
+
+// Residue planes of an integer operand, laid out as residue_kernel's
+// unsliced planes (A: plane l row i at i * kp; B: plane l row p at
+// (s_max - 1) * kp + p, np bytes per row).  rows x cols of the source from
+// src (already at the chunk's first k); padding is zero.
+template <int EB, bool ROWS_A>
+__global__ void __launch_bounds__(256) int_residue_kernel(const char *src, int64_t s_r, int64_t s_c,
+                                                          uint64_t rows, uint64_t cols, uint64_t kp,
+                                                          uint64_t np, int s_max, const CrtHdr *h,
+                                                          int8_t *planes, uint64_t plane_bytes) {
+    const int nmod = h->nmod;
+    if (nmod == 0) return;
+    const uint64_t R = ROWS_A ? rows : kp, C = ROWS_A ? kp : np;
+    const uint64_t chunks = C / 4, total = R * chunks;
+    for (uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * 256) {
+        const uint64_t r = idx / chunks, c0 = (idx % chunks) * 4;
+        int64_t v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint64_t sc = c0 + e;
+            v[e] = (r < rows && sc < cols) ? load_ielem<EB>(src, (int64_t)r * s_r + (int64_t)sc * s_c) : 0;
+        }
+        int8_t *dst = ROWS_A ? planes + r * ((uint64_t)s_max * kp) + c0
+                             : planes + ((uint64_t)(s_max - 1) * kp + r) * np + c0;
+        for (int l = 0; l < nmod; ++l) {
+            uint32_t wd = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                wd |= (uint32_t)(uint8_t)(int8_t)(v[e] ? int_residue(v[e], l) : 0) << (8 * e);
+            *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = wd;
+        }
+    }
+}
+
+// The exact sum of one cell by the plain loop (driver::gemm,
+// crates/uor-matmul-gemm/src/driver.rs:67-182).
+template <int EB>
+__device__ inline W192 int_direct_sum(const IArgs &F, uint64_t i, uint64_t j) {
+    W192 x{{0, 0, 0}};
+    const int64_t ab = (int64_t)i * F.ars, bb = (int64_t)j * F.bcs;
+    for (uint64_t p = 0; p < F.k; ++p) {
+        const int64_t a = load_ielem<EB>(F.a, ab + (int64_t)p * F.acs);
+        const int64_t b = load_ielem<EB>(F.b, (int64_t)p * F.brs + bb);
+        if constexpr (EB <= 4) w192_add(x, (i128)(a * b));  // |a * b| <= 2^62
+        else w192_add(x, (i128)a * (i128)b);
+    }
+    return x;
+}
+
+// Linear::finish and the one encode (epilogue.rs:67-95; acc.rs:128-150 for
+// i128, impl_encode_from_limbs acc.rs:405-442 for Limbs<3>).
+template <int OB>
+__device__ inline void int_finish(const IArgs &F, char *cp, const W192 &x) {
+    const i128 low = (i128)(((u128)x.w[1] << 64) | x.w[0]);
+    if (!F.limbs) {
+        // i16 / i32 elements: |X| < 2^126, the i128 accumulator.
+        i128 t = sat_mul(low, F.alpha);
+        if (F.beta != 0) t = (i128)((u128)t + (u128)sat_mul(load_out<OB>(cp), F.beta));
+        store_out<OB>(cp, encode_int(t, OB, F.mode));
+        return;
+    }
+    if (F.mode == UOR_ENCODE_WRAPPING) {
+        store_out<OB>(cp, encode_int(low, OB, UOR_ENCODE_WRAPPING));
+        return;
+    }
+    const bool neg = (int64_t)x.w[2] < 0;
+    uint64_t m0 = x.w[0], m1 = x.w[1], m2 = x.w[2];
+    if (neg) {
+        m0 = ~m0;
+        m1 = ~m1;
+        m2 = ~m2;
+        u128 t = (u128)m0 + 1;
+        m0 = (uint64_t)t;
+        t = (u128)m1 + (uint64_t)(t >> 64);
+        m1 = (uint64_t)t;
+        m2 += (uint64_t)(t >> 64);
+    }
+    i128 mn, mx;
+    out_range(OB, &mn, &mx);
+    const u128 mag = ((u128)m1 << 64) | m0;
+    const u128 limit = neg ? (u128)0 - (u128)mn : (u128)mx;
+    i128 v;
+    if (m2 != 0 || mag > limit) v = neg ? mn : mx;
+    else v = neg ? (i128)((u128)0 - mag) : (i128)mag;
+    store_out<OB>(cp, v);
+}
+
+template <int ND>
+__device__ inline W192 crt_w192(const uint8_t *y, uint64_t y_plane, uint64_t cell, int nmod) {
+    uint32_t D[ND];
+    const bool neg = crt16<ND>(y, y_plane, cell, nmod, D);
+    // |X| < 2^192 (B <= 192), so the digits past the twelfth are zero.
+    uint64_t w[3] = {0, 0, 0};
+#pragma unroll
+    for (int d = 0; d < ND && d < 12; ++d) w[d / 4] |= (uint64_t)D[d] << (16 * (d % 4));
+    W192 x{{w[0], w[1], w[2]}};
+    if (neg) {
+        x.w[0] = ~x.w[0];
+        x.w[1] = ~x.w[1];
+        x.w[2] = ~x.w[2];
+        u128 t = (u128)x.w[0] + 1;
+        x.w[0] = (uint64_t)t;
+        t = (u128)x.w[1] + (uint64_t)(t >> 64);
+        x.w[1] = (uint64_t)t;
+        x.w[2] += (uint64_t)(t >> 64);
+    }
+    return x;
+}
+
+// One thread per cell of a 4 x 64 tile: the CRT reconstruction (or, with no
+// header, with crt_off, the per-cell loop), then the epilogue.
+template <int EB>
+__global__ void __launch_bounds__(256) int_finish_kernel(IArgs F, const LineStat *ra,
+                                                         const LineStat *cb, const CrtHdr *h,
+                                                         const uint8_t *y, uint64_t y_plane,
+                                                         int gn) {
+    const int t = threadIdx.x;
+    const uint64_t i = (uint64_t)(blockIdx.x / gn) * 4 + t / 64;
+    const uint64_t j = (uint64_t)(blockIdx.x % gn) * 64 + t % 64;
+    if (i >= F.m || j >= F.n) return;
+    W192 x{{0, 0, 0}};
+    if (!h || h->crt_off) {
+        x = int_direct_sum<EB>(F, i, j);
+    } else {
+        const int nmod = h->nmod;
+        if (nmod > 0 && !((ra[i].flags | cb[j].flags) & LS_EMPTY)) {
+            const uint64_t cell = i * F.n + j;
+            const int nd = crt_nd16[nmod];
+            if (nd <= 8) x = crt_w192<8>(y, y_plane, cell, nmod);
+            else if (nd <= 12) x = crt_w192<12>(y, y_plane, cell, nmod);
+            else x = crt_w192<16>(y, y_plane, cell, nmod);
+        }
+    }
+    char *cp = F.c + ((int64_t)i * F.crs + (int64_t)j * F.ccs) * F.ob;
+    switch (F.ob) {
+    case 1: int_finish<1>(F, cp, x); break;
+    case 2: int_finish<2>(F, cp, x); break;
+    case 4: int_finish<4>(F, cp, x); break;
+    case 8: int_finish<8>(F, cp, x); break;
+    default: int_finish<16>(F, cp, x); break;
+    }
+}
+
+// Moduli planes enough for any data of EB-byte elements at depth k: B <=
+// 2 * 8 * EB + ceil(log2 k) bits, and each of the first 30 moduli adds at
+// least 7 bits of capacity.
+static int int_moduli_cap(int eb, uint64_t k) {
+    int lk = 0;
+    while (lk < 64 && (1ull << lk) < k) ++lk;
+    const int need = 16 * eb + lk;
+    return std::min(CRT_NMAX, (need + 6) / 7 + 1);
+}
+
+template <int EB>
+static hipError_t launch_int_crt(const IArgs &F, char *scratch, const CrtLayout &L, uint64_t kc,
+                                 hipStream_t s) {
+    const uint64_t m = F.m, k = F.k, n = F.n;
+    const int nm = L.nm;
+    CrtHdr *h = (CrtHdr *)(scratch + L.hdr);
+    LineStat *ra = (LineStat *)(scratch + L.ra), *cb = (LineStat *)(scratch + L.cb);
+    int8_t *ap = (int8_t *)(scratch + L.ap), *bp = (int8_t *)(scratch + L.bp);
+    uint8_t *y = (uint8_t *)(scratch + L.y);
+    // 1. line statistics over the whole depth.
+    if (F.acs == 1)
+        hipLaunchKernelGGL((int_line_stats_kernel<EB, true>), dim3((unsigned)m), dim3(256), 0, s, F.a, F.ars,
+                           F.acs, m, k, ra);
+    else
+        hipLaunchKernelGGL((int_line_stats_kernel<EB, false>), dim3((unsigned)((m + 15) / 16)), dim3(256), 0,
+                           s, F.a, F.ars, F.acs, m, k, ra);
+    if (F.brs == 1)
+        hipLaunchKernelGGL((int_line_stats_kernel<EB, true>), dim3((unsigned)n), dim3(256), 0, s, F.b, F.bcs,
+                           F.brs, n, k, cb);
+    else
+        hipLaunchKernelGGL((int_line_stats_kernel<EB, false>), dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
+                           s, F.b, F.bcs, F.brs, n, k, cb);
+    // 2. plan (never sliced: every line is at most 64 bits wide).
+    hipLaunchKernelGGL(crt_plan_kernel, dim3(1), dim3(256), 0, s, ra, m, cb, n, k, nm, 1, 1, h);
+    // 3-4. per chunk of at most kc: residue planes, residue GEMMs.
+    constexpr int BM = 256, BN = 256;
+    const int gm = (int)((m + BM - 1) / BM), gn = (int)((n + BN - 1) / BN);
+    const auto blocks = [](uint64_t t) { return (unsigned)std::min<uint64_t>((t + 255) / 256, 4096); };
+    for (uint64_t k0 = 0; k0 < k; k0 += kc) {
+        const uint64_t kl = std::min(kc, k - k0);
+        const uint64_t ta = m * (L.kp / 4), tb = L.kp * (L.np / 4);
+        hipLaunchKernelGGL((int_residue_kernel<EB, true>), dim3(blocks(ta)), dim3(256), 0, s,
+                           F.a + (int64_t)k0 * F.acs * EB, F.ars, F.acs, m, kl, L.kp, L.np, 1, h, ap, L.a_plane);
+        hipLaunchKernelGGL((int_residue_kernel<EB, false>), dim3(blocks(tb)), dim3(256), 0, s,
+                           F.b + (int64_t)k0 * F.brs * EB, F.brs, F.bcs, kl, n, L.kp, L.np, 1, h, bp, L.b_plane);
+        // (The GEMM runs over the layout's whole kp: a short last chunk's
+        // padding residues are zero.)
+        ResOut R{y, L.y_plane, nm, ap, bp, L.a_plane, L.b_plane, L.kp, L.np, 1, 1, h, k0 > 0 ? 1 : 0};
+        const dim3 grid((unsigned)(gm * gn), 1, (unsigned)nm);
+        hipLaunchKernelGGL((residue_gemm_kernel<BM, BN, 2, 4, true>), grid, dim3(512), 0, s, m, n, gm, gn, R);
+    }
+    // 5. reconstruction, epilogue, encode.
+    const uint64_t fm = (m + 3) / 4, fn = (n + 63) / 64;
+    hipLaunchKernelGGL((int_finish_kernel<EB>), dim3((unsigned)(fm * fn)), dim3(256), 0, s, F, ra, cb, h, y,
+                       L.y_plane, (int)fn);
+    return hipGetLastError();
+}
+
+template <int EB>
+static hipError_t launch_int_direct(const IArgs &F, hipStream_t s) {
+    const uint64_t fm = (F.m + 3) / 4, fn = (F.n + 63) / 64;
+    hipLaunchKernelGGL((int_finish_kernel<EB>), dim3((unsigned)(fm * fn)), dim3(256), 0, s, F, nullptr, nullptr,
+                       nullptr, nullptr, 0, (int)fn);
+    return hipGetLastError();
+}
+
 }  // namespace uor
 
 using namespace uor;
@@ -1416,4 +1764,88 @@ extern "C" int uor_gfx950_dgemm(uint64_t m, uint64_t k, uint64_t n, int64_t alph
                                 uint64_t scratch_bytes, void *stream) {
     return raw_gemm(1, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, scratch,
                     scratch_bytes, stream);
+}
+
+extern "C" uint64_t uor_gfx950_suggested_scratch_int(int elem_bytes, uint64_t m, uint64_t k,
+                                                     uint64_t n) {
+    if (elem_bytes == 1) return uor_gfx950_suggested_scratch_i8(m, k, n);
+    if (!(elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8)) return 0;
+    if (m == 0 || n == 0 || k == 0) return 0;
+    const uint64_t kc = std::min<uint64_t>(k, CRT_BK_MAX);
+    return crt_layout(m, kc, n, int_moduli_cap(elem_bytes, k), 1).total + 256;
+}
+
+extern "C" int uor_gfx950_gemm_int(int elem_bytes, const uor_view *a, const uor_view *b,
+                                   const uor_view *c, int out_type, int64_t alpha, int64_t beta,
+                                   int encode, void *scratch, uint64_t scratch_bytes, void *stream,
+                                   uor_route *route) {
+    if (elem_bytes == 1)
+        return uor_gfx950_gemm_i8(a, b, c, out_type, alpha, beta, encode, scratch, scratch_bytes, stream,
+                                  route);
+    route_set(route, UOR_ROUTE_NONE);
+    if (!(elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8) || !valid_out_type(out_type) ||
+        !valid_encode(encode))
+        return UOR_INVALID_ARGUMENT;
+    Placed A, B, C;
+    int st = make_triple(a, elem_bytes, b, elem_bytes, c, out_type, &A, &B, &C);
+    if (st) return st;
+    if (C.rows == 0 || C.cols == 0) return UOR_OK;
+    // Limbs<3>'s scale and prior rules are not restated: i64 elements take
+    // alpha = 1, beta = 0 only.
+    if (elem_bytes == 8 && !(alpha == 1 && beta == 0)) return UOR_INVALID_ARGUMENT;
+    const uintptr_t oalign = (uintptr_t)(out_type < 8 ? out_type : 8) - 1;
+    if ((((uintptr_t)A.base | (uintptr_t)B.base) & (uintptr_t)(elem_bytes - 1)) || ((uintptr_t)C.base & oalign))
+        return UOR_INVALID_ARGUMENT;
+    IArgs F{A.base, A.rs, A.cs, B.base, B.rs, B.cs, C.base, C.rs, C.cs, A.rows, A.cols, B.cols,
+            alpha, beta, encode, out_type, elem_bytes == 8 ? 1 : 0};
+    hipStream_t s = (hipStream_t)stream;
+    // The residue route when the offer holds planes: as many moduli as the
+    // element width can need at this depth, or as many as fit (the device
+    // plan sends every cell to the per-cell loop if the data needs more).
+    int nm = 0;
+    CrtLayout L{};
+    char *sc = nullptr;
+    const uint64_t kc = std::min<uint64_t>(F.k, CRT_BK_MAX);
+    if (scratch && F.k > 0) {
+        const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+        const uint64_t have = scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
+        sc = (char *)p1;
+        for (int q = int_moduli_cap(elem_bytes, F.k); q >= 1; --q) {
+            const CrtLayout Lq = crt_layout(F.m, kc, F.n, q, 1);
+            if (Lq.total <= have) {
+                nm = q;
+                L = Lq;
+                break;
+            }
+        }
+        const uint64_t gm = (F.m + 255) / 256, gn = (F.n + 255) / 256;
+        if (gm * gn > 0x7fffffffull || F.m > 0x7fffffffull || F.n > 0x7fffffffull) nm = 0;
+    }
+    if (nm > 0) {
+        UOR_HIP(elem_bytes == 2   ? launch_int_crt<2>(F, sc, L, kc, s)
+                : elem_bytes == 4 ? launch_int_crt<4>(F, sc, L, kc, s)
+                                  : launch_int_crt<8>(F, sc, L, kc, s));
+        if (route) {
+            route->kind = UOR_ROUTE_INT_CRT;
+            route->tile_m = route->tile_n = 256;
+            route->tile_k = DL_BK;
+            route->split_k = (int)((F.k + kc - 1) / kc);  // depth chunks
+            route->launches = 4 + 3 * route->split_k;
+            route->moduli = nm;
+            route->scratch_used = L.total;
+        }
+        return UOR_OK;
+    }
+    if ((F.m + 3) / 4 * ((F.n + 63) / 64) > 0x7fffffffull) return UOR_INVALID_ARGUMENT;
+    UOR_HIP(elem_bytes == 2   ? launch_int_direct<2>(F, s)
+            : elem_bytes == 4 ? launch_int_direct<4>(F, s)
+                              : launch_int_direct<8>(F, s));
+    if (route) {
+        route->kind = F.k == 0 ? UOR_ROUTE_EPILOGUE_ONLY : UOR_ROUTE_INT_DIRECT;
+        route->tile_m = 4;
+        route->tile_n = 64;
+        route->split_k = 1;
+        route->launches = 1;
+    }
+    return UOR_OK;
 }

@@ -22,7 +22,8 @@ ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
           4: "invalid_argument"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
-          10: "lut4_dot4", 11: "lut4_mfma", 20: "float_crt", 21: "float_direct", 30: "trop_valu"}
+          10: "lut4_dot4", 11: "lut4_mfma", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
+          40: "int_crt", 41: "int_direct"}
 
 # Every symbol include/uor_gfx950.h declares.
 SYMBOLS = [
@@ -31,6 +32,8 @@ SYMBOLS = [
     "uor_gfx950_slice_gemm_ex_i8",
     "uor_gfx950_slice_gemm_i8",
     "uor_gfx950_suggested_scratch_i8",
+    "uor_gfx950_gemm_int",
+    "uor_gfx950_suggested_scratch_int",
     "uor_gfx950_gemm_lut4",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
@@ -92,6 +95,12 @@ def lib():
         L.uor_gfx950_slice_gemm_i8.restype = _i32
         L.uor_gfx950_suggested_scratch_i8.argtypes = [_u64, _u64, _u64]
         L.uor_gfx950_suggested_scratch_i8.restype = _u64
+        if hasattr(L, "uor_gfx950_gemm_int"):
+            L.uor_gfx950_gemm_int.argtypes = [_i32, _PV, _PV, _PV, _i32, _i64, _i64, _i32, _vp,
+                                              _u64, _vp, _PR]
+            L.uor_gfx950_gemm_int.restype = _i32
+            L.uor_gfx950_suggested_scratch_int.argtypes = [_i32, _u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_int.restype = _u64
         if hasattr(L, "uor_gfx950_gemm_lut4"):
             L.uor_gfx950_gemm_lut4.argtypes = [_PV, _vp, _u64, _u64, _vp, _u64, _u64, _PV, _i32,
                                                _i64, _i64, _i32, _vp, _u64, _vp, _PR]
@@ -172,6 +181,29 @@ def slice_gemm_i8(m, k, n, a, b, c, out="i32", scratch=None, stream=None):
 
 def suggested_scratch_i8(m, k, n):
     return lib().uor_gfx950_suggested_scratch_i8(m, k, n)
+
+
+def gemm_int(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+             out="i64", alpha=1, beta=0, encode="nearest", scratch=None, stream=None):
+    """The view API at E = i8/i16/i32/i64 (the element width from a's dtype).
+    Returns (status, route dict).  `c` is a flat device tensor of the output
+    type (int8/16/32/64, or int64 pairs for i128)."""
+    eb = a.element_size()
+    ob = OUT[out]
+    rec = 2 if ob == 16 else 1
+    av = view(a, *a_shape, *a_strides)
+    bv = view(b, *b_shape, *b_strides)
+    cv = view(c, *c_shape, *c_strides, rec=rec)
+    r = Route()
+    st = lib().uor_gfx950_gemm_int(eb, ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob,
+                                   int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
+                                   0 if scratch is None else scratch.numel() * scratch.element_size(),
+                                   _stream(stream), ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def suggested_scratch_int(elem_bytes, m, k, n):
+    return lib().uor_gfx950_suggested_scratch_int(elem_bytes, m, k, n)
 
 
 def gemm_lut4(a, m, k, a_strides, codes, n, books, group, c, c_strides, out="i32", alpha=1,
