@@ -393,6 +393,67 @@ def bench_float(args, torch, uor, gen):
     return out
 
 
+def bench_int(args, torch, uor):
+    """The i16/i32/i64 element families (uor_gfx950_gemm_int): full-range
+    random operands, alpha = 1, beta = 0, outputs wide enough to be exact (i64
+    for i16 elements, i128 for i32 and i64).  Timed on the residue route with
+    the suggested offer; 64 rows checked bit for bit against the per-cell
+    route (no offer) on the same operands."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(21)
+    out = []
+    for eb, N, outt in ((2, 4096, "i64"), (4, 4096, "i128"), (8, 2048, "i128")):
+        dt = {2: torch.int16, 4: torch.int32, 8: torch.int64}[eb]
+        info = torch.iinfo(dt)
+        a = torch.randint(info.min, info.max, (N * N,), dtype=dt, device=dev, generator=g)
+        b = torch.randint(info.min, info.max, (N * N,), dtype=dt, device=dev, generator=g)
+        rec = 2 if outt == "i128" else 1
+        c = torch.zeros(N * N * rec, dtype=torch.int64, device=dev)
+        size = uor.suggested_scratch_int(eb, N, N, N)
+        sc = torch.empty(size, dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream()
+        route = {}
+
+        def step():
+            st, r = uor.gemm_int(a, (N, N), (N, 1), b, (N, N), (N, 1), c, (N, N), (N, 1), out=outt,
+                                 scratch=sc, stream=stream.cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"gemm_int status {st}")
+            route.update(r)
+
+        step()
+        torch.cuda.synchronize()
+        settle(torch, step)
+        steps = max(1, min(args.steps, 10))
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(steps):
+            step()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / steps
+        R = 64
+        slab = torch.zeros(R * N * rec, dtype=torch.int64, device=dev)
+        st, _ = uor.gemm_int(a, (R, N), (N, 1), b, (N, N), (N, 1), slab, (R, N), (N, 1), out=outt)
+        torch.cuda.synchronize()
+        parity = st == 0 and bool(torch.equal(slab, c[:R * N * rec]))
+        off = (-sc.data_ptr()) % 256
+        plan = sc[off:off + 12].cpu().view(torch.int32).tolist()
+        nmod = plan[0]
+        kp = (N + 63) // 64 * 64
+        issued = 2.0 * N * N * kp * nmod / (ms * 1e-3) / 1e12
+        out.append({"elements": f"i{8 * eb}", "m": N, "n": N, "k": N, "out": outt,
+                    "route": route.get("kind"), "ms_per_call": round(ms, 4),
+                    "exact_TOPS": round(2.0 * N ** 3 / (ms * 1e-3) / 1e12, 2),
+                    "moduli": nmod, "bound_bits": plan[2],
+                    "int8_TOPS_issued": round(issued, 1),
+                    "frac_int8_mfma_peak": round(issued / PEAK_INT8_TOPS, 4),
+                    "parity_vs_direct_route_64_rows": parity})
+        del a, b, c, sc, slab
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline_i8(host, oracle):
     """The reference's packed route restated (oracle/fastroute.cpp) on a row
     slab of the same 8192^3 problem, all usable host cores."""
@@ -438,6 +499,7 @@ def main():
     ap.add_argument("--no-lut", action="store_true", help="skip the secondary LUT decode figure")
     ap.add_argument("--no-trop", action="store_true", help="skip the secondary max-plus figure")
     ap.add_argument("--no-float", action="store_true", help="skip the secondary exact-float figure")
+    ap.add_argument("--no-int", action="store_true", help="skip the i16/i32/i64 element figure")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device-to-device copy and exit (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -490,6 +552,13 @@ def main():
             "metric": "exact float GEMM TFLOP/s (2mnk per second, rounded once)",
             "config": "BASELINE configs[3]",
             "runs": bench_float(args, torch, uor, gen),
+        }
+    if not args.no_int:
+        log("[bench] i16/i32/i64 elements")
+        result["integer"] = {
+            "metric": "exact integer GEMM TOPS (2mnk per second), i16/i32/i64 elements",
+            "config": "SURVEY 8(f) rank 1: the Kernelized i16/i32/i64 families, full-range operands",
+            "runs": bench_int(args, torch, uor),
         }
     if not args.no_cpu_baseline:
         from oracle import oracle

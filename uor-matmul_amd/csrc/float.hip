@@ -494,19 +494,20 @@ __device__ inline void trim(const Dec &d, uint64_t *m, int *x) {
 __device__ inline int bitlen64(uint64_t v) { return 64 - __builtin_clzll(v); }
 
 // Statistics of `lines` lines of `len` elements: element e of line t at
-// base + t * s_line + e * s_elem.  CONTIG (s_elem == 1): one workgroup per
-// line, threads along it; otherwise 16 lines per workgroup, 16 consecutive
-// threads across them (coalesced when s_line == 1) and 16 lanes along each.
-template <bool F64, bool CONTIG>
+// base + t * s_line + e * s_elem.  LPB lines per workgroup, thread t on line
+// t % LPB at elements t / LPB, + 256 / LPB, ...: LPB = 1 (s_elem == 1) puts
+// the threads along one line; LPB = 64 (s_line == 1) puts a wave across 64
+// neighbouring lines, one 64-element row segment per load; LPB = 16 is for
+// the other strides.
+template <bool F64, int LPB>
 __global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64_t s_line,
                                                          int64_t s_elem, uint64_t lines,
                                                          uint64_t len, LineStat *out) {
-    constexpr int LPB = CONTIG ? 1 : 16;  // lines per block
-    constexpr int TPL = 256 / LPB;        // threads per line
+    constexpr int TPL = 256 / LPB;  // threads per line
     __shared__ int s_lo[256], s_hi[256], s_fl[256];
     __shared__ double s_sum[256];
     const int t = threadIdx.x;
-    const int tl = CONTIG ? 0 : (t & 15), te = CONTIG ? t : (t >> 4);
+    const int tl = t % LPB, te = t / LPB;
     const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
     const bool live = line < lines;
     int lo = 1 << 30, hi = -(1 << 30), fl = 0;
@@ -531,7 +532,7 @@ __global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64
     __syncthreads();
     for (int w = TPL / 2; w >= 1; w >>= 1) {
         if (te < w) {
-            const int o = CONTIG ? t + w : t + 16 * w;
+            const int o = t + LPB * w;
             s_lo[t] = min(s_lo[t], s_lo[o]);
             s_hi[t] = max(s_hi[t], s_hi[o]);
             s_fl[t] |= s_fl[o];
@@ -557,7 +558,7 @@ __global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64
     s_sum[t] = sum;
     __syncthreads();
     for (int w = TPL / 2; w >= 1; w >>= 1) {
-        if (te < w) s_sum[t] += s_sum[CONTIG ? t + w : t + 16 * w];
+        if (te < w) s_sum[t] += s_sum[t + LPB * w];
         __syncthreads();
     }
     if (te == 0 && live) {
@@ -1208,6 +1209,21 @@ static int crt_slice_cap(bool f64, uint64_t k) {
     return s;
 }
 
+// Line statistics with the lanes along a line when it is contiguous, else
+// 16 lines by 16 lanes.  (64 lines by 4 lanes, one 64-element row segment
+// per load, ran 5x slower at 4096 lines of 4096: 64 workgroups whose lanes
+// each wait on 1024 loads in turn.)
+template <bool F64>
+static void launch_line_stats(const char *base, int64_t s_line, int64_t s_elem, uint64_t lines,
+                              uint64_t len, LineStat *out, hipStream_t s) {
+    if (s_elem == 1)
+        hipLaunchKernelGGL((line_stats_kernel<F64, 1>), dim3((unsigned)lines), dim3(256), 0, s, base, s_line,
+                           s_elem, lines, len, out);
+    else
+        hipLaunchKernelGGL((line_stats_kernel<F64, 16>), dim3((unsigned)((lines + 15) / 16)), dim3(256), 0, s,
+                           base, s_line, s_elem, lines, len, out);
+}
+
 template <bool F64>
 static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, hipStream_t s) {
     const uint64_t m = F.m, k = F.k, n = F.n;
@@ -1217,18 +1233,8 @@ static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, 
     int8_t *ap = (int8_t *)(scratch + L.ap), *bp = (int8_t *)(scratch + L.bp);
     uint8_t *y = (uint8_t *)(scratch + L.y);
     // 1. line statistics: rows of A (elements along acs), columns of B (along brs).
-    if (F.acs == 1)
-        hipLaunchKernelGGL((line_stats_kernel<F64, true>), dim3((unsigned)m), dim3(256), 0, s, F.a, F.ars,
-                           F.acs, m, k, ra);
-    else
-        hipLaunchKernelGGL((line_stats_kernel<F64, false>), dim3((unsigned)((m + 15) / 16)), dim3(256), 0,
-                           s, F.a, F.ars, F.acs, m, k, ra);
-    if (F.brs == 1)
-        hipLaunchKernelGGL((line_stats_kernel<F64, true>), dim3((unsigned)n), dim3(256), 0, s, F.b, F.bcs,
-                           F.brs, n, k, cb);
-    else
-        hipLaunchKernelGGL((line_stats_kernel<F64, false>), dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
-                           s, F.b, F.bcs, F.brs, n, k, cb);
+    launch_line_stats<F64>(F.a, F.ars, F.acs, m, k, ra, s);
+    launch_line_stats<F64>(F.b, F.bcs, F.brs, n, k, cb, s);
     // 2. plan.
     hipLaunchKernelGGL(crt_plan_kernel, dim3(1), dim3(256), 0, s, ra, m, cb, n, k, nm, L.sa_max,
                        L.sb_max, h);
@@ -1326,16 +1332,15 @@ __device__ inline void w192_add(W192 &x, i128 v) {
 
 // Line statistics of integer lines: lo = 0, width = bit length of the
 // largest magnitude, l1 an upper bound of log2 of the sum of magnitudes.
-template <int EB, bool CONTIG>
+template <int EB, int LPB>
 __global__ void __launch_bounds__(256) int_line_stats_kernel(const char *base, int64_t s_line,
                                                              int64_t s_elem, uint64_t lines,
                                                              uint64_t len, LineStat *out) {
-    constexpr int LPB = CONTIG ? 1 : 16;  // lines per block
-    constexpr int TPL = 256 / LPB;        // threads per line
+    constexpr int TPL = 256 / LPB;  // threads per line (as line_stats_kernel)
     __shared__ int s_hi[256];
     __shared__ double s_sum[256];
     const int t = threadIdx.x;
-    const int tl = CONTIG ? 0 : (t & 15), te = CONTIG ? t : (t >> 4);
+    const int tl = t % LPB, te = t / LPB;
     const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
     const bool live = line < lines;
     int hi = 0;
@@ -1347,7 +1352,7 @@ __global__ void __launch_bounds__(256) int_line_stats_kernel(const char *base, i
     s_hi[t] = hi;
     __syncthreads();
     for (int w = TPL / 2; w >= 1; w >>= 1) {
-        if (te < w) s_hi[t] = max(s_hi[t], s_hi[CONTIG ? t + w : t + 16 * w]);
+        if (te < w) s_hi[t] = max(s_hi[t], s_hi[t + LPB * w]);
         __syncthreads();
     }
     hi = s_hi[tl];
@@ -1360,7 +1365,7 @@ __global__ void __launch_bounds__(256) int_line_stats_kernel(const char *base, i
     s_sum[t] = sum;
     __syncthreads();
     for (int w = TPL / 2; w >= 1; w >>= 1) {
-        if (te < w) s_sum[t] += s_sum[CONTIG ? t + w : t + 16 * w];
+        if (te < w) s_sum[t] += s_sum[t + LPB * w];
         __syncthreads();
     }
     if (te == 0 && live) {
@@ -1392,18 +1397,27 @@ __device__ inline uint32_t umod_p(uint32_t x, int l) {
     return (uint32_t)r;
 }
 
-// The balanced int8 residue of v modulo crt_mod[l].
+// The balanced int8 residue of an EB-byte element v modulo crt_mod[l].
+template <int EB>
 __device__ inline int int_residue(int64_t v, int l) {
     const uint64_t a = mag64(v);
+    const int p = crt_mod[l];
     int r;
     if (l == 0) {
         r = (int)(a & 255);
+    } else if constexpr (EB == 2) {
+        // a <= 2^15: a float quotient is off by at most one.
+        const int q = (int)((float)a * crt_invpf[l]);
+        r = (int)a - q * p;
+        if (r < 0) r += p;
+        if (r >= p) r -= p;
+    } else if constexpr (EB == 4) {
+        r = (int)umod_p((uint32_t)a, l);  // a <= 2^31
     } else {
-        const uint32_t p32 = umod_p(umod_p(65536u, l) * umod_p(65536u, l), l);  // 2^32 mod p
+        const uint32_t p32 = crt_pow2[l][32];  // 2^32 mod p
         const uint32_t rh = umod_p((uint32_t)(a >> 32), l), rl = umod_p((uint32_t)a, l);
         r = (int)umod_p(rh * p32 + rl, l);
     }
-    const int p = crt_mod[l];
     int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
     if (v < 0) b = -b;
     if (b == 128) b = -128;  // p = 256: 128 and -128 are one residue
@@ -1438,7 +1452,7 @@ __global__ void __launch_bounds__(256) int_residue_kernel(const char *src, int64
             uint32_t wd = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                wd |= (uint32_t)(uint8_t)(int8_t)(v[e] ? int_residue(v[e], l) : 0) << (8 * e);
+                wd |= (uint32_t)(uint8_t)(int8_t)(v[e] ? int_residue<EB>(v[e], l) : 0) << (8 * e);
             *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = wd;
         }
     }
@@ -1466,6 +1480,10 @@ __device__ inline void int_finish(const IArgs &F, char *cp, const W192 &x) {
     const i128 low = (i128)(((u128)x.w[1] << 64) | x.w[0]);
     if (!F.limbs) {
         // i16 / i32 elements: |X| < 2^126, the i128 accumulator.
+        if (F.alpha == 1 && F.beta == 0) {
+            store_out<OB>(cp, encode_int(low, OB, F.mode));
+            return;
+        }
         i128 t = sat_mul(low, F.alpha);
         if (F.beta != 0) t = (i128)((u128)t + (u128)sat_mul(load_out<OB>(cp), F.beta));
         store_out<OB>(cp, encode_int(t, OB, F.mode));
@@ -1573,18 +1591,16 @@ static hipError_t launch_int_crt(const IArgs &F, char *scratch, const CrtLayout 
     int8_t *ap = (int8_t *)(scratch + L.ap), *bp = (int8_t *)(scratch + L.bp);
     uint8_t *y = (uint8_t *)(scratch + L.y);
     // 1. line statistics over the whole depth.
-    if (F.acs == 1)
-        hipLaunchKernelGGL((int_line_stats_kernel<EB, true>), dim3((unsigned)m), dim3(256), 0, s, F.a, F.ars,
-                           F.acs, m, k, ra);
-    else
-        hipLaunchKernelGGL((int_line_stats_kernel<EB, false>), dim3((unsigned)((m + 15) / 16)), dim3(256), 0,
-                           s, F.a, F.ars, F.acs, m, k, ra);
-    if (F.brs == 1)
-        hipLaunchKernelGGL((int_line_stats_kernel<EB, true>), dim3((unsigned)n), dim3(256), 0, s, F.b, F.bcs,
-                           F.brs, n, k, cb);
-    else
-        hipLaunchKernelGGL((int_line_stats_kernel<EB, false>), dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
-                           s, F.b, F.bcs, F.brs, n, k, cb);
+    const auto stats = [&](const char *base, int64_t s_line, int64_t s_elem, uint64_t lines, LineStat *out) {
+        if (s_elem == 1)
+            hipLaunchKernelGGL((int_line_stats_kernel<EB, 1>), dim3((unsigned)lines), dim3(256), 0, s, base,
+                               s_line, s_elem, lines, k, out);
+        else
+            hipLaunchKernelGGL((int_line_stats_kernel<EB, 16>), dim3((unsigned)((lines + 15) / 16)), dim3(256),
+                               0, s, base, s_line, s_elem, lines, k, out);
+    };
+    stats(F.a, F.ars, F.acs, m, ra);
+    stats(F.b, F.bcs, F.brs, n, cb);
     // 2. plan (never sliced: every line is at most 64 bits wide).
     hipLaunchKernelGGL(crt_plan_kernel, dim3(1), dim3(256), 0, s, ra, m, cb, n, k, nm, 1, 1, h);
     // 3-4. per chunk of at most kc: residue planes, residue GEMMs.
