@@ -85,6 +85,7 @@ typedef struct uor_view {
 #define UOR_ROUTE_MFMA_WIDE 4     /* int8 MFMA, i64 register widening */
 #define UOR_ROUTE_LUT4_DOT4 10    /* 4-bit table-lookup, v_perm decode, dot4 (small m) */
 #define UOR_ROUTE_LUT4_MFMA 11    /* 4-bit table-lookup, v_perm decode into int8 MFMA */
+#define UOR_ROUTE_LUT4_PREFILL 12 /* 4-bit table-lookup, many rows: decode W^T, dense int8 MFMA */
 #define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
 #define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
 #define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */
@@ -189,12 +190,19 @@ uint64_t uor_gfx950_suggested_scratch_int(int elem_bytes, uint64_t m, uint64_t k
  * a per-group codebook is ceil(n/group) reference calls over 128-row
  * CodedMatrix slices and MatViewMut column windows of C; group == n is one.
  * c: m x n view of `out_type` elements.  Epilogue and encode as gemm_i8.
+ * For m >= 128, an offer of uor_gfx950_suggested_scratch_lut4 bytes decodes
+ * W^T once into it and runs the dense int8 route (the reference's
+ * decode-then-multiply spelling of the same value, coded.rs:98-140, CD-13);
+ * any smaller offer, the table-lookup kernels.  The bytes are the same.
  */
 int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uint64_t codes_len,
                          uint64_t n, const int8_t *books, uint64_t books_len,
                          uint64_t group, const uor_view *c, int out_type,
                          int64_t alpha, int64_t beta, int encode, void *scratch,
                          uint64_t scratch_bytes, void *stream, uor_route *route);
+
+/* The offer that lets gemm_lut4 take the decode-then-dense route (0 below m = 128). */
+uint64_t uor_gfx950_suggested_scratch_lut4(uint64_t m, uint64_t k, uint64_t n);
 
 /* =================================================== exact float GEMM */
 

@@ -16,7 +16,7 @@ def to_dev(x, dev):
 
 
 def run_case(oracle, uor, dev, m, k, n, group, seed, out=np.int32, alpha=1, beta=0,
-             encode="nearest", a_strides=None, code_offset=0, expect=None):
+             encode="nearest", a_strides=None, code_offset=0, expect=None, offer=False):
     rng = np.random.default_rng(seed)
     ars, acs = a_strides or (k, 1)
     alen = 1 + max(0, (m - 1) * abs(ars) + (k - 1) * abs(acs)) if m and k else 0
@@ -30,8 +30,13 @@ def run_case(oracle, uor, dev, m, k, n, group, seed, out=np.int32, alpha=1, beta
     gc = to_dev(c0, dev)
     gcodes = to_dev(codes, dev)[code_offset:]
     ost = {np.int8: "i8", np.int16: "i16", np.int32: "i32", np.int64: "i64"}[out]
+    scratch = None
+    if offer:
+        nbytes = uor.suggested_scratch_lut4(m, k, n)
+        scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
     gst, route = uor.gemm_lut4(to_dev(a, dev), m, k, (ars, acs), gcodes, n, to_dev(books, dev),
-                               group, gc, (n, 1), out=ost, alpha=alpha, beta=beta, encode=encode)
+                               group, gc, (n, 1), out=ost, alpha=alpha, beta=beta, encode=encode,
+                               scratch=scratch)
     torch.cuda.synchronize()
     assert uor.STATUS.get(gst, gst) == st
     assert np.array_equal(gc.cpu().numpy(), want), (m, k, n, group, route)
@@ -159,6 +164,40 @@ def test_tiles_per_cu(uor, dev, m, k, n):
     st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1))
     torch.cuda.synchronize()
     assert st == 0 and route["kind"] == "lut4_mfma" and route["split_k"] == 1, route
+    W = decode_torch(codes, n, k, books, group).to(torch.float64)
+    want = a.view(m, k).to(torch.float64) @ W.T
+    assert torch.equal(c.view(m, n).to(torch.float64), want), route
+
+
+@pytest.mark.parametrize("m,k,n,group,out,alpha,beta,code_offset", [
+    (128, 2048, 96, 32, np.int32, 1, 0, 0), (200, 1000, 333, 7, np.int64, 3, -1, 0),
+    (130, 256, 45, 4, np.int16, 1 << 40, -(1 << 35), 3), (300, 130, 1000, 128, np.int8, 3, -1, 0)])
+def test_prefill_decode_then_dense(oracle, uor, dev, m, k, n, group, out, alpha, beta, code_offset):
+    """m >= 128 with the suggested offer: W^T decoded once into the offer,
+    then the dense int8 route (ragged n, k not a multiple of the 32-weight
+    decode chunk, unaligned code rows, every output width's epilogue).  The
+    same bytes as the oracle; without the offer the table-lookup kernels."""
+    route = run_case(oracle, uor, dev, m, k, n, group, seed=m + n, out=out, alpha=alpha, beta=beta,
+                     code_offset=code_offset, offer=True)
+    assert route["kind"] == "lut4_prefill", route
+    route = run_case(oracle, uor, dev, m, k, n, group, seed=m + n, out=out, alpha=alpha, beta=beta,
+                     code_offset=code_offset)
+    assert route["kind"] != "lut4_prefill", route
+
+
+def test_prefill_config_shape(uor, dev):
+    """The config 3 weights (k = 8192, n = 28672, 224 codebooks) at m = 512 on
+    the decode-then-dense route, against a decode in torch and a float64
+    matmul (exact: every sum is an integer below 2^53)."""
+    m, k, n, group = 512, 8192, 28672, 128
+    a = to_dev(gen.i8_full(m * k, 6), dev)
+    codes = to_dev(gen.i8_full(n * k // 2, 7).view(np.uint8), dev)
+    books = to_dev(gen.i8_full((n // group) * 16, 8), dev)
+    c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    scratch = torch.empty(uor.suggested_scratch_lut4(m, k, n), dtype=torch.uint8, device=dev)
+    st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1), scratch=scratch)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "lut4_prefill", route
     W = decode_torch(codes, n, k, books, group).to(torch.float64)
     want = a.view(m, k).to(torch.float64) @ W.T
     assert torch.equal(c.view(m, n).to(torch.float64), want), route

@@ -774,6 +774,57 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
     }
 }
 
+// ------------------------------------------- many rows: decode, then dense
+//
+// For m >= LUT_PREFILL_M the weights are decoded once into W^T (k x n int8,
+// row-major, leading dimension ldw, a multiple of 16) and the product runs on
+// the dense int8 MFMA route: the reference's decode-then-multiply spelling of
+// the same value (coded_gemm, crates/uor-matmul-gemm/src/coded.rs:98-140;
+// `decline`, tabulated.rs:2555-2745; CD-13).  A workgroup decodes a tile of
+// 128 columns x 128 weights into LDS ([k][column]: thread t owns column t %
+// 128 and 64 of the weights), then writes the tile's 128 rows of W^T as
+// 128-byte row segments (8 lanes x 16 bytes per row).
+constexpr uint64_t LUT_PREFILL_M = 128;
+
+__global__ void __launch_bounds__(256) lut4_decode_t_kernel(LutArgs L, int book_aligned, int code_fast,
+                                                            int8_t *wt, uint64_t ldw) {
+    __shared__ __attribute__((aligned(16))) int8_t tile[128][128];
+    const int t = threadIdx.x;
+    const uint64_t j0 = (uint64_t)blockIdx.x * 128, k0 = (uint64_t)blockIdx.y * 128;
+    {
+        const int cl = t & 127, kh = t >> 7;  // column in the tile, half of the tile's depth
+        const uint64_t j = j0 + cl;
+        if (j < L.n) {
+            uint32_t q0, q1, q2, q3;
+            load_book(L, j, book_aligned, q0, q1, q2, q3);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kt = 64 * kh + 32 * h;  // first weight of this chunk in the tile
+                const uint4 cw = codes16(L, j, (k0 + kt) / 2, code_fast != 0);
+                const uint32_t w[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    uint32_t e, o;
+                    decode8(w[d], q0, q1, q2, q3, L.sel_mask, L.sel_base, e, o);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        tile[kt + 8 * d + 2 * b][cl] = (int8_t)(e >> (8 * b));
+                        tile[kt + 8 * d + 2 * b + 1][cl] = (int8_t)(o >> (8 * b));
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int ch = t & 7;  // 16-byte chunk of a 128-byte row segment
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int r = pass * 32 + (t >> 3);
+        const uint64_t kk = k0 + r, jc = j0 + 16 * ch;
+        if (kk < L.k && jc < ldw) *(uint4 *)(wt + kk * ldw + jc) = *(const uint4 *)&tile[r][16 * ch];
+    }
+}
+
 }  // namespace uor
 
 using namespace uor;
@@ -783,8 +834,6 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
                                     uint64_t group, const uor_view *c, int out_type, int64_t alpha,
                                     int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
                                     void *stream, uor_route *route) {
-    (void)scratch;
-    (void)scratch_bytes;
     route_set(route, UOR_ROUTE_NONE);
     if (!valid_out_type(out_type) || !valid_encode(encode)) return UOR_INVALID_ARGUMENT;
     if (!a || !c) return UOR_INVALID_ARGUMENT;
@@ -823,6 +872,30 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         route->operand_modes = fast;
     }
     const bool a16 = A.cs == 1 && ((uintptr_t)A.base % 16 == 0) && (A.rs % 16 == 0 || m == 1);
+    // m >= LUT_PREFILL_M with an offer that holds W^T: decode, then the dense
+    // int8 route (whatever is left of the offer goes to it).
+    const uint64_t ldw = (n + 15) / 16 * 16;
+    if (m >= LUT_PREFILL_M && scratch && k > 0 && k <= (1ull << 40) / ldw) {
+        const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+        const uint64_t have = scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
+        const uint64_t wbytes = (k * ldw + 255) & ~255ull;
+        if (wbytes <= have && (n + 127) / 128 <= 0x7fffffffull && (k + 127) / 128 <= 65535) {
+            int8_t *wt = (int8_t *)p1;
+            const dim3 grid((unsigned)((n + 127) / 128), (unsigned)((k + 127) / 128));
+            hipLaunchKernelGGL(lut4_decode_t_kernel, grid, dim3(256), 0, s, L, book_aligned, (int)code_fast, wt,
+                               ldw);
+            UOR_HIP(hipGetLastError());
+            const uor_view bv{wt, k * ldw, k, n, (int64_t)ldw, 1};
+            const int st2 = uor_gfx950_gemm_i8(a, &bv, c, out_type, alpha, beta, encode, wt + wbytes,
+                                               have - wbytes, stream, route);
+            if (route && st2 == UOR_OK) {
+                route->kind = UOR_ROUTE_LUT4_PREFILL;
+                route->launches += 1;
+                route->scratch_used += wbytes;
+            }
+            return st2;
+        }
+    }
     // 2 <= m <= 32, whole 2048-weight blocks, k <= 65536 (each wave's i32 sum
     // over the whole depth is exact), 16-byte aligned code rows (all below
     // 2^31 bytes) and activation rows: one workgroup per CU with the
@@ -908,4 +981,12 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
     hipLaunchKernelGGL(lut4_mfma_kernel, dim3((unsigned)tiles), dim3(256), 0, s, L, fast, book_aligned, kq);
     UOR_HIP(hipGetLastError());
     return UOR_OK;
+}
+
+extern "C" uint64_t uor_gfx950_suggested_scratch_lut4(uint64_t m, uint64_t k, uint64_t n) {
+    // W^T for the decode-then-dense route (m >= LUT_PREFILL_M), plus the
+    // dense route's own offer; none below (the LUT kernels use no scratch).
+    if (m < LUT_PREFILL_M || k == 0 || n == 0) return 0;
+    const uint64_t ldw = (n + 15) / 16 * 16;
+    return 256 + ((k * ldw + 255) & ~255ull) + uor_gfx950_suggested_scratch_i8(m, k, n);
 }

@@ -22,7 +22,7 @@ ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
           4: "invalid_argument"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
-          10: "lut4_dot4", 11: "lut4_mfma", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
+          10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
           40: "int_crt", 41: "int_direct"}
 
 # Every symbol include/uor_gfx950.h declares.
@@ -35,6 +35,7 @@ SYMBOLS = [
     "uor_gfx950_gemm_int",
     "uor_gfx950_suggested_scratch_int",
     "uor_gfx950_gemm_lut4",
+    "uor_gfx950_suggested_scratch_lut4",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
     "uor_gfx950_sgemm",
@@ -105,6 +106,8 @@ def lib():
             L.uor_gfx950_gemm_lut4.argtypes = [_PV, _vp, _u64, _u64, _vp, _u64, _u64, _PV, _i32,
                                                _i64, _i64, _i32, _vp, _u64, _vp, _PR]
             L.uor_gfx950_gemm_lut4.restype = _i32
+            L.uor_gfx950_suggested_scratch_lut4.argtypes = [_u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_lut4.restype = _u64
         if hasattr(L, "uor_gfx950_gemm_float"):
             L.uor_gfx950_gemm_float.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32, _vp, _u64,
                                                 _vp, _PR]
@@ -218,6 +221,10 @@ def gemm_lut4(a, m, k, a_strides, codes, n, books, group, c, c_strides, out="i32
         0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
         ctypes.byref(r))
     return st, r.as_dict()
+
+
+def suggested_scratch_lut4(m, k, n):
+    return lib().uor_gfx950_suggested_scratch_lut4(m, k, n)
 
 
 def gemm_float(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides, alpha=1,
