@@ -274,6 +274,49 @@ def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
     return out
 
 
+def bench_lut_prefill(args, torch, uor, gen, m=2048):
+    """SURVEY 8(f) rank 2, LUT prefill: the config 3 weights (k = 8192,
+    n = 28672, 224 codebooks) at m = 2048 rows with the suggested offer: W^T
+    decoded once per call, then the dense int8 route.  Checked against the
+    table-lookup route (no offer) on the same call."""
+    k, n, group = 8192, 28672, 128
+    dev = torch.device("cuda:0")
+    codes = torch.from_numpy(gen.i8_full(n * k // 2, 7).view("uint8")).to(dev)
+    books = torch.from_numpy(gen.i8_full((n // group) * 16, 8)).to(dev)
+    a = torch.from_numpy(gen.i8_full(m * k, 6)).to(dev)
+    c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    sc = torch.empty(uor.suggested_scratch_lut4(m, k, n), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    route = {}
+
+    def step(scr=sc, cc=c):
+        st, r = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, cc, (n, 1), scratch=scr,
+                              stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"lut4 status {st}")
+        route.update(r)
+
+    step()
+    torch.cuda.synchronize()
+    settle(torch, step)
+    steps = max(1, min(args.steps, 20))
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(steps):
+        step()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    ms = s0.elapsed_time(s1) / steps
+    kind = route.get("kind")
+    ref = torch.zeros_like(c)
+    step(None, ref)
+    torch.cuda.synchronize()
+    tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"m": m, "k": k, "n": n, "group": group, "route": kind, "ms_per_call": round(ms, 4),
+            "TOPS": round(tops, 1), "frac_int8_mfma_peak": round(tops / PEAK_INT8_TOPS, 4),
+            "parity_vs_lut_route": bool(torch.equal(c, ref))}
+
+
 def bench_trop(args, torch, uor, gen):
     """Trop<i8> max-plus GEMM at m = n = k = 4096, 5% of entries
     at the semiring zero, output Trop<i32>.  One term is one (+, max) pair;
@@ -538,6 +581,7 @@ def main():
             "config": "BASELINE configs[2]: 4-bit codes, k=8192, n=28672, group=128, "
                       "3 rotating code buffers (>256 MB MALL)",
             "runs": lut,
+            "prefill": bench_lut_prefill(args, torch, uor, gen),
         }
     if not args.no_trop:
         log("[bench] trop max-plus")
