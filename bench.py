@@ -337,32 +337,64 @@ def bench_trop(args, torch, uor, gen):
 
     a, b = recs(11), recs(12)
     c = torch.zeros(N * N * 8, dtype=torch.uint8, device=dev)
+    c_sel = torch.zeros(N * N * 8, dtype=torch.uint8, device=dev)
+    w = torch.zeros(N * N, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream()
 
-    def step():
+    def plain():
         st, _ = uor.gemm_trop_i8(a, (N, N), (N, 1), b, (N, N), (N, 1), c, (N, N), (N, 1),
                                  stream=stream.cuda_stream)
         if st != 0:
             raise RuntimeError(f"trop status {st}")
 
-    for _ in range(max(1, args.warmup)):
-        step()
-    torch.cuda.synchronize()
-    settle(torch, step)
-    steps = max(10, min(args.steps, 50))
-    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s0.record(stream)
-    for _ in range(steps):
-        step()
-    s1.record(stream)
-    torch.cuda.synchronize()
-    ms = s0.elapsed_time(s1) / steps
+    def selected():
+        st, _ = uor.gemm_trop_i8_selected(a, (N, N), (N, 1), b, (N, N), (N, 1), c_sel, (N, N),
+                                          (N, 1), w, (N, 1), stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"trop selected status {st}")
+
+    def timed(step):
+        for _ in range(max(1, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        settle(torch, step)
+        steps = max(10, min(args.steps, 50))
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(steps):
+            step()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1) / steps
+
     terms = float(N) ** 3
+    ms = timed(plain)
     rate = terms / (ms * 1e-3)
+    ms_sel = timed(selected)
+    rate_sel = terms / (ms_sel * 1e-3)
+    # The witness route's C must be the plain route's bytes, and each witness
+    # must attain its cell's value (a gather over all cells).
+    rec_i32 = c_sel.view(N * N, 8)
+    vals = rec_i32[:, :4].contiguous().view(torch.int32).view(N, N)
+    fin = rec_i32[:, 4].view(N, N) != 0
+    av = a.view(N, N, 2)
+    bv = b.view(N, N, 2)
+    W = w.view(N, N)
+    rows = torch.arange(N, device=dev)[:, None].expand(N, N)
+    cols = torch.arange(N, device=dev)[None, :].expand(N, N)
+    ta = av[rows, W]
+    tb = bv[W, cols]
+    term = ta[..., 0].view(torch.int8).int() + tb[..., 0].view(torch.int8).int()
+    attain = bool(((term == vals) & (ta[..., 1] != 0) & (tb[..., 1] != 0) | ~fin).all())
     return {"m": N, "n": N, "k": N, "out": "Trop<i32>", "ms_per_call": round(ms, 5),
             "terms_per_s": round(rate / 1e12, 3), "unit": "Tterm/s",
             "peak": PEAK_TROP_TERMS / 1e12, "frac_valu": round(rate / PEAK_TROP_TERMS, 4),
-            "kernel": "trop_i8_kernel", "bound": "valu"}
+            "kernel": "trop_i8_kernel<true, false>", "bound": "valu",
+            "selected": {"ms_per_call": round(ms_sel, 5), "terms_per_s": round(rate_sel / 1e12, 3),
+                         "frac_valu": round(rate_sel / PEAK_TROP_TERMS, 4),
+                         "kernel": "trop_i8_kernel<true, true>", "witness": "u64, least index",
+                         "values_equal_plain": bool(torch.equal(c_sel, c)),
+                         "witness_attains_value": attain}}
 
 
 def bench_float(args, torch, uor, gen):

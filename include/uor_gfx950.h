@@ -89,6 +89,8 @@ typedef struct uor_view {
 #define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
 #define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
 #define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */
+#define UOR_ROUTE_TROP_SELECTED 31        /* max-plus + witness, (value, index) keys, VALU */
+#define UOR_ROUTE_TROP_SELECTED_DIRECT 32 /* max-plus + witness, per-cell loop (k > 2^21) */
 #define UOR_ROUTE_INT_CRT 40      /* i16/i32/i64 elements: int8 residue MFMA + CRT */
 #define UOR_ROUTE_INT_DIRECT 41   /* i16/i32/i64 elements: per-cell exact loop */
 typedef struct uor_route {
@@ -277,6 +279,34 @@ int uor_gfx950_gemm_trop_i8(const uor_view *a, const uor_view *b, const uor_view
                             int64_t beta, int beta_finite, int encode,
                             void *scratch, uint64_t scratch_bytes, void *stream,
                             uor_route *route);
+
+/* Witness mechanisms (uor_matmul_gemm::Witness, selection.rs:45-56); both
+ * give identical bytes (CD-25): the least index attaining the maximum. */
+#define UOR_WITNESS_LEXICOGRAPHIC 0
+#define UOR_WITNESS_COMPARE_PASS 1
+
+/*
+ * gemm_selected(&mut SelectedTriple, &MaxPlus{alpha,beta}, GemmOptions{encode},
+ * mechanism, ..) at E = Trop<i8>, O = Trop<out>
+ * (crates/uor-matmul-gemm/src/selection.rs:212-320): C as
+ * uor_gfx950_gemm_trop_i8 writes it, and
+ *
+ *   W[i,j] := the least p with A[i,p] + B[p,j] equal to the maximum
+ *
+ * over the same terms, a term touching -inf counting as -inf (so a cell whose
+ * every term is -inf has witness 0), and 0 at k == 0 (selection.rs:264-268).
+ * w: view of uint64 elements (usize on a 64-bit target), 8-byte aligned.
+ * Status order: the a, b, c checks of uor_gfx950_gemm_trop_i8, then the
+ * witness (SelectedTriple::new, selection.rs:76-98): SHORT_BUFFER,
+ * NONCONFORMANT when it is not m x n, OUTPUT_ALIASES_ITSELF.
+ */
+int uor_gfx950_gemm_trop_i8_selected(const uor_view *a, const uor_view *b,
+                                     const uor_view *c, const uor_view *w,
+                                     int out_type, int64_t alpha, int alpha_finite,
+                                     int64_t beta, int beta_finite, int encode,
+                                     int mechanism, void *scratch,
+                                     uint64_t scratch_bytes, void *stream,
+                                     uor_route *route);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,8 @@ def lib():
         L.ora_gemm_float.restype = _i32
         L.ora_gemm_trop.argtypes = [_i32] + _VIEW * 3 + [_i32, _i64, _i32, _i64, _i32, _i32]
         L.ora_gemm_trop.restype = _i32
+        L.ora_gemm_trop_selected.argtypes = [_i32] + _VIEW * 4 + [_i32, _i64, _i32, _i64, _i32, _i32]
+        L.ora_gemm_trop_selected.restype = _i32
         _lib = L
     return _lib
 
@@ -132,6 +134,22 @@ def gemm_trop(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_stride
                              *_view(c, *c_shape, *c_strides, rec=2 * out_bytes),
                              out_bytes, int(alpha[0]), int(bool(alpha[1])),
                              int(beta[0]), int(bool(beta[1])), ENCODE[encode])
+    return STATUS[st]
+
+
+def gemm_trop_selected(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+                       w, w_strides, alpha=(0, True), beta=(0, False), encode="nearest",
+                       elem_bytes=1, out_bytes=4):
+    """gemm_selected (Lexicographic) over Trop records: as gemm_trop, plus the
+    witness `w`, a uint64 array viewed as an m x n matrix with w_strides."""
+    m, n = c_shape
+    st = lib().ora_gemm_trop_selected(elem_bytes,
+                                      *_view(a, *a_shape, *a_strides, rec=2 * elem_bytes),
+                                      *_view(b, *b_shape, *b_strides, rec=2 * elem_bytes),
+                                      *_view(c, *c_shape, *c_strides, rec=2 * out_bytes),
+                                      *_view(w, m, n, *w_strides),
+                                      out_bytes, int(alpha[0]), int(bool(alpha[1])),
+                                      int(beta[0]), int(bool(beta[1])), ENCODE[encode])
     return STATUS[st]
 
 

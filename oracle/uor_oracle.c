@@ -652,3 +652,60 @@ int ora_gemm_trop(int elem_bytes,
     }
     return ORA_OK;
 }
+
+/*
+ * gemm_selected (crates/uor-matmul-gemm/src/selection.rs:170-320), the
+ * Lexicographic mechanism: per cell, the maximum of the (value, index) pairs
+ * under the order "greater value, then smaller index" (Lex::combine,
+ * selection.rs:115-153), a term at the semiring zero standing at i128::MIN;
+ * C gets MaxPlus::finish of the value, W the index, min(index, k) (an empty
+ * reduction's index is k = 0).  The witness view has 8-byte (usize) cells and
+ * is checked like C (SelectedTriple::new, selection.rs:72-97).
+ */
+int ora_gemm_trop_selected(int elem_bytes,
+                           const void *a, uint64_t a_len, uint64_t a_rows, uint64_t a_cols, int64_t a_rs, int64_t a_cs,
+                           const void *b, uint64_t b_len, uint64_t b_rows, uint64_t b_cols, int64_t b_rs, int64_t b_cs,
+                           void *c, uint64_t c_len, uint64_t c_rows, uint64_t c_cols, int64_t c_rs, int64_t c_cs,
+                           uint64_t *w, uint64_t w_len, uint64_t w_rows, uint64_t w_cols, int64_t w_rs, int64_t w_cs,
+                           int out_bytes, int64_t alpha, int alpha_finite, int64_t beta, int beta_finite, int mode) {
+    if (!(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8)) return ORA_INVALID_ARGUMENT;
+    if (!(out_bytes == 1 || out_bytes == 2 || out_bytes == 4 || out_bytes == 8)) return ORA_INVALID_ARGUMENT;
+    if (mode < 0 || mode > 3) return ORA_INVALID_ARGUMENT;
+    view_t A = {a, a_len, a_rows, a_cols, a_rs, a_cs, 0};
+    view_t B = {b, b_len, b_rows, b_cols, b_rs, b_cs, 0};
+    view_t C = {c, c_len, c_rows, c_cols, c_rs, c_cs, 0};
+    int st = make_triple(&A, &B, &C);
+    if (st) return st;
+    view_t W = {w, w_len, w_rows, w_cols, w_rs, w_cs, 0};
+    if (!ora_place(W.len, W.rows, W.cols, W.rs, W.cs, &W.origin)) return ORA_SHORT_BUFFER;
+    if (W.rows != A.rows || W.cols != B.cols) return ORA_NONCONFORMANT;
+    if (ora_self_aliases(W.rows, W.cols, W.rs, W.cs)) return ORA_OUTPUT_ALIASES_ITSELF;
+    uint64_t m = A.rows, k = A.cols, n = B.cols;
+    i128 mn, mx;
+    int_range(out_bytes, &mn, &mx);
+    for (uint64_t i = 0; i < m; i++) {
+        for (uint64_t j = 0; j < n; j++) {
+            i128 v = I128_MIN;
+            uint64_t idx = UINT64_MAX;  /* Lex::EMPTY */
+            for (uint64_t p = 0; p < k; p++) {
+                int fa, fb;
+                i128 x = trop_load(a, at(&A, i, p), elem_bytes, &fa);
+                i128 y = trop_load(b, at(&B, p, j), elem_bytes, &fb);
+                i128 t = (fa && fb) ? x + y : I128_MIN;
+                if (t > v || (t == v && p < idx)) { v = t; idx = p; }
+            }
+            i128 total = (v != I128_MIN && alpha_finite) ? v + alpha : I128_MIN;
+            uint64_t ci = at(&C, i, j);
+            if (beta_finite) {
+                int fc;
+                i128 cv = trop_load(c, ci, out_bytes, &fc);
+                i128 prior = fc ? cv + beta : I128_MIN;
+                if (prior > total) total = prior;
+            }
+            if (total == I128_MIN) trop_store(c, ci, out_bytes, 0, 0);
+            else trop_store(c, ci, out_bytes, 1, encode_i128_into(total, mn + 1, mx - 1, mode));
+            w[at(&W, i, j)] = idx < k ? idx : k;
+        }
+    }
+    return ORA_OK;
+}

@@ -86,3 +86,80 @@ def test_encode_clamps_to_min_plus_one(oracle):
                      encode="wrapping")
     # 200 wraps over span 254 starting at -127: (200 + 127) % 254 - 127 = -54
     assert c.view(np.int8)[0] == -54
+
+
+# ------------------------------------------------------ gemm_selected witness
+
+def sel(oracle, av, af, bv, bf, m, k, n, alpha=(0, True), beta=(0, False), c0=None):
+    a = oracle.trop_bytes(oracle.trop_i8(np.asarray(av), np.asarray(af, bool)))
+    b = oracle.trop_bytes(oracle.trop_i8(np.asarray(bv), np.asarray(bf, bool)))
+    c = np.zeros(m * n, dtype=oracle.TROP_I32) if c0 is None else c0.copy()
+    cb = oracle.trop_bytes(c) if m * n else np.zeros(0, np.uint8)
+    w = np.full(m * n, 7777, np.uint64)
+    st = oracle.gemm_trop_selected(a if a.size else np.zeros(0, np.uint8), (m, k), (k, 1),
+                                   b if b.size else np.zeros(0, np.uint8), (k, n), (n, 1),
+                                   cb, (m, n), (n, 1), w, (n, 1), alpha=alpha, beta=beta)
+    return st, (cb.view(oracle.TROP_I32) if m * n else c), w
+
+
+def test_selected_doc_example(oracle):
+    # selection.rs:186-211 and its tie test: 1+9 and 9+1 both give 10; D-6
+    # takes the smaller index.
+    st, c, w = sel(oracle, [1, 9], [1, 1], [9, 1], [1, 1], 1, 2, 1)
+    assert st == "ok" and c["finite"][0] and c["value"][0] == 10 and w[0] == 0
+
+
+def test_selected_degenerate_ct04(oracle):
+    # selection.rs the_degenerate_selections_are_answers_ct_04: every term
+    # masked -> NEG_INF with witness 0; depth zero -> NEG_INF with witness 0.
+    st, c, w = sel(oracle, [0] * 4, [0] * 4, [0] * 4, [0] * 4, 1, 4, 1)
+    assert st == "ok" and not c["finite"][0] and w[0] == 0
+    st, c, w = sel(oracle, [], [], [], [], 1, 0, 1)
+    assert st == "ok" and not c["finite"][0] and w[0] == 0
+
+
+def test_selected_nonconformant_and_aliasing_ct05(oracle):
+    a = oracle.trop_bytes(oracle.trop_i8(np.array([1, 2]), np.ones(2, bool)))
+    b = oracle.trop_bytes(oracle.trop_i8(np.array([3, 4]), np.ones(2, bool)))
+    cb = oracle.trop_bytes(np.zeros(1, dtype=oracle.TROP_I32))
+    w = np.zeros(4, np.uint64)
+    # A 2x2 witness for a 1x1 product (selection.rs:236-250).
+    st = oracle.lib().ora_gemm_trop_selected(
+        1, *oracle._view(a, 1, 2, 2, 1, rec=2), *oracle._view(b, 2, 1, 1, 1, rec=2),
+        *oracle._view(cb, 1, 1, 1, 1, rec=8), *oracle._view(w, 2, 2, 2, 1), 4, 0, 1, 0, 0, 0)
+    assert oracle.STATUS[st] == "nonconformant"
+    c4 = oracle.trop_bytes(np.zeros(4, dtype=oracle.TROP_I32))
+    st = oracle.lib().ora_gemm_trop_selected(
+        1, *oracle._view(a, 2, 1, 1, 1, rec=2), *oracle._view(b, 1, 2, 2, 1, rec=2),
+        *oracle._view(c4, 2, 2, 2, 1, rec=8), *oracle._view(w, 2, 2, 0, 1), 4, 0, 1, 0, 0, 0)
+    assert oracle.STATUS[st] == "output_aliases_itself"
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_selected_brute_force_with_ties(oracle, seed):
+    """Values from a small range force ties; the witness is the least p whose
+    term attains the maximum (every term masked: 0), and C is gemm_trop's."""
+    rng = np.random.default_rng(seed)
+    m, k, n = 5, 23, 6
+    av, bv = rng.integers(-3, 4, m * k), rng.integers(-3, 4, k * n)
+    af, bf = rng.random(m * k) > 0.25, rng.random(k * n) > 0.25
+    af[:k] = False  # row 0 fully masked
+    st, c, w = sel(oracle, av, af, bv, bf, m, k, n)
+    assert st == "ok"
+    A, B = av.reshape(m, k), bv.reshape(k, n)
+    AF, BF = af.reshape(m, k), bf.reshape(k, n)
+    for i in range(m):
+        for j in range(n):
+            terms = [A[i, p] + B[p, j] if AF[i, p] and BF[p, j] else None for p in range(k)]
+            fin = [t for t in terms if t is not None]
+            if fin:
+                best = max(fin)
+                assert c["finite"][i * n + j] and c["value"][i * n + j] == best
+                assert w[i * n + j] == terms.index(best)
+            else:
+                assert not c["finite"][i * n + j] and w[i * n + j] == 0
+    plain = oracle.trop_bytes(np.zeros(m * n, dtype=oracle.TROP_I32))
+    a = oracle.trop_bytes(oracle.trop_i8(av, af))
+    b = oracle.trop_bytes(oracle.trop_i8(bv, bf))
+    oracle.gemm_trop(a, (m, k), (k, 1), b, (k, n), (n, 1), plain, (m, n), (n, 1))
+    assert np.array_equal(plain.view(oracle.TROP_I32), c)

@@ -23,7 +23,8 @@ STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buf
           4: "invalid_argument"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
           10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
-          40: "int_crt", 41: "int_direct"}
+          31: "trop_selected", 32: "trop_selected_direct", 40: "int_crt", 41: "int_direct"}
+WITNESS = {"lexicographic": 0, "compare_pass": 1}
 
 # Every symbol include/uor_gfx950.h declares.
 SYMBOLS = [
@@ -42,6 +43,7 @@ SYMBOLS = [
     "uor_gfx950_dgemm",
     "uor_gfx950_suggested_scratch_float",
     "uor_gfx950_gemm_trop_i8",
+    "uor_gfx950_gemm_trop_i8_selected",
 ]
 
 
@@ -127,6 +129,10 @@ def lib():
             L.uor_gfx950_gemm_trop_i8.argtypes = [_PV, _PV, _PV, _i32, _i64, _i32, _i64, _i32,
                                                   _i32, _vp, _u64, _vp, _PR]
             L.uor_gfx950_gemm_trop_i8.restype = _i32
+            L.uor_gfx950_gemm_trop_i8_selected.argtypes = [_PV, _PV, _PV, _PV, _i32, _i64, _i32,
+                                                           _i64, _i32, _i32, _i32, _vp, _u64, _vp,
+                                                           _PR]
+            L.uor_gfx950_gemm_trop_i8_selected.restype = _i32
         _lib = L
     return _lib
 
@@ -279,6 +285,26 @@ def gemm_trop_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_str
     st = lib().uor_gfx950_gemm_trop_i8(
         ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), out, int(alpha[0]),
         int(bool(alpha[1])), int(beta[0]), int(bool(beta[1])), ENCODE[encode], _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def gemm_trop_i8_selected(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+                          w, w_strides, out=4, alpha=(0, True), beta=(0, False), encode="nearest",
+                          mechanism="lexicographic", w_shape=None, scratch=None, stream=None):
+    """gemm_selected at E = Trop<i8>: as gemm_trop_i8, plus the witness `w`, a
+    flat int64/uint64 device tensor viewed as w_shape (default c_shape) with
+    w_strides."""
+    av = view(a, *a_shape, *a_strides, rec=2)
+    bv = view(b, *b_shape, *b_strides, rec=2)
+    cv = view(c, *c_shape, *c_strides, rec=2 * out)
+    wv = view(w, *(w_shape or c_shape), *w_strides)
+    r = Route()
+    st = lib().uor_gfx950_gemm_trop_i8_selected(
+        ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ctypes.byref(wv), out,
+        int(alpha[0]), int(bool(alpha[1])), int(beta[0]), int(bool(beta[1])), ENCODE[encode],
+        WITNESS.get(mechanism, mechanism), _ptr(scratch),
         0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
         ctypes.byref(r))
     return st, r.as_dict()
