@@ -275,7 +275,7 @@ def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
 
 
 def bench_lut_prefill(args, torch, uor, gen, m=2048):
-    """SURVEY 8(f) rank 2, LUT prefill: the config 3 weights (k = 8192,
+    """LUT prefill: the config 3 weights (k = 8192,
     n = 28672, 224 codebooks) at m = 2048 rows with the suggested offer: W^T
     decoded once per call, then the dense int8 route.  Checked against the
     table-lookup route (no offer) on the same call."""
@@ -315,6 +315,58 @@ def bench_lut_prefill(args, torch, uor, gen, m=2048):
     return {"m": m, "k": k, "n": n, "group": group, "route": kind, "ms_per_call": round(ms, 4),
             "TOPS": round(tops, 1), "frac_int8_mfma_peak": round(tops / PEAK_INT8_TOPS, 4),
             "parity_vs_lut_route": bool(torch.equal(c, ref))}
+
+
+def bench_coded(args, torch, uor, gen):
+    """Coded operands beyond the 4-bit grid: Ternary<4, u8> weights (2-bit
+    digits, four per byte) at the config 3 shape (k = 8192, n = 28672, W
+    n x k as gemm_tabulated declares it), at m = 1 and m = 2048, with the
+    suggested offer: W decoded once per call into the scratch, then the dense
+    int8 route.  Parity: the decode-free per-cell route on 16 output rows of
+    the same call (the direct route over all rows would take seconds)."""
+    import numpy as np
+    k, n = 8192, 28672
+    dev = torch.device("cuda:0")
+    codes = torch.from_numpy(gen.i8_full(n * k // 4, 21).view("uint8")).to(dev)
+    cd = uor.codec("ternary", code_bits=8, block=4)
+    stream = torch.cuda.current_stream()
+    runs = []
+    for m in (1, 2048):
+        a = torch.from_numpy(gen.i8_full(m * k, 22)).to(dev)
+        c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+        sc = torch.empty(uor.suggested_scratch_coded(m, k, n), dtype=torch.uint8, device=dev)
+        route = {}
+
+        def step():
+            st, r = uor.gemm_coded(a, (m, k), (k, 1), cd, codes, n, k, True, c, (m, n), (n, 1),
+                                   scratch=sc, stream=stream.cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"coded status {st}")
+            route.update(r)
+
+        step()
+        torch.cuda.synchronize()
+        settle(torch, step)
+        steps = max(1, min(args.steps, 20))
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(steps):
+            step()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / steps
+        rows = min(m, 16)
+        ref = torch.zeros(rows * n, dtype=torch.int32, device=dev)
+        st, _ = uor.gemm_coded(a, (rows, k), (k, 1), cd, codes, n, k, True, ref, (rows, n),
+                               (n, 1), stream=stream.cuda_stream)
+        torch.cuda.synchronize()
+        tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        runs.append({"m": m, "k": k, "n": n, "codec": "Ternary<4, u8>", "route": route.get("kind"),
+                     "ms_per_call": round(ms, 4), "TOPS": round(tops, 2),
+                     "code_bytes": n * k // 4,
+                     "parity_vs_direct_rows": rows if st == 0 and torch.equal(c[:rows * n], ref)
+                     else False})
+    return runs
 
 
 def bench_trop(args, torch, uor, gen):
@@ -614,6 +666,7 @@ def main():
                       "3 rotating code buffers (>256 MB MALL)",
             "runs": lut,
             "prefill": bench_lut_prefill(args, torch, uor, gen),
+            "ternary": bench_coded(args, torch, uor, gen),
         }
     if not args.no_trop:
         log("[bench] trop max-plus")
@@ -633,7 +686,7 @@ def main():
         log("[bench] i16/i32/i64 elements")
         result["integer"] = {
             "metric": "exact integer GEMM TOPS (2mnk per second), i16/i32/i64 elements",
-            "config": "SURVEY 8(f) rank 1: the Kernelized i16/i32/i64 families, full-range operands",
+            "config": "the Kernelized i16/i32/i64 families, full-range operands",
             "runs": bench_int(args, torch, uor),
         }
     if not args.no_cpu_baseline:

@@ -86,6 +86,8 @@ typedef struct uor_view {
 #define UOR_ROUTE_LUT4_DOT4 10    /* 4-bit table-lookup, v_perm decode, dot4 (small m) */
 #define UOR_ROUTE_LUT4_MFMA 11    /* 4-bit table-lookup, v_perm decode into int8 MFMA */
 #define UOR_ROUTE_LUT4_PREFILL 12 /* 4-bit table-lookup, many rows: decode W^T, dense int8 MFMA */
+#define UOR_ROUTE_CODED_DENSE 13  /* any fixed-width codec: decode W into scratch, dense int8 route */
+#define UOR_ROUTE_CODED_DIRECT 14 /* any fixed-width codec, no offer: per-cell decode and sum */
 #define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
 #define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
 #define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */
@@ -205,6 +207,71 @@ int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uint64_t codes
 
 /* The offer that lets gemm_lut4 take the decode-then-dense route (0 below m = 128). */
 uint64_t uor_gfx950_suggested_scratch_lut4(uint64_t m, uint64_t k, uint64_t n);
+
+/* ======================================== coded operands, any fixed-width tier */
+
+/* Codec tiers over the i8 alphabet (crates/uor-matmul-codec/src/codecs.rs). */
+#define UOR_TIER_IDENTITY 0 /* code = the value (int8)                     :42-57   */
+#define UOR_TIER_GRID 1     /* table[code % entries], u16 codes            :80-104  */
+#define UOR_TIER_BOOK 2     /* table[(code % entries) * block + i % block]  :268-309 */
+#define UOR_TIER_SIGN 3     /* bit i % block of the code: 1 -> +1, else -1  :362-401 */
+#define UOR_TIER_TERNARY 4  /* digit i % block: 0 -> -1, 2 -> +1, 1/3 -> 0  :466-517 */
+
+/*
+ * A constructed codec (Codec<i8, Bd>, codecs.rs), as the GPU reads it:
+ *
+ *   base tier   tier, entries (N), block (BLK), code_bits (the code type K:
+ *               8 for u8, 16 for u16; Identity 8, Grid 16), table (device,
+ *               int8: N entries for Grid, N * BLK for Book; NULL otherwise)
+ *   packed      P in {1, 2, 4, 8}: Packed<base, P> (codecs.rs:150-200):
+ *               stored codes are u8 holding P sub-codes of 8/P bits, the low
+ *               sub-code first (CK-03); 0: the base codes are stored as is
+ *   has_zero    Offset<.., zero> over the above (codecs.rs:566-620): the
+ *               decoded value minus zero, i8 wrapping_sub
+ *
+ * The codec constructors' own checks (Sign/Ternary/Offset::new bounds) are
+ * the caller's; the library checks only what the decode needs.
+ */
+typedef struct uor_codec {
+    int32_t tier;
+    int32_t code_bits;
+    int32_t packed;
+    int32_t has_zero;
+    int64_t zero;
+    uint64_t entries;
+    uint64_t block;
+    const int8_t *table;
+    uint64_t table_len;
+} uor_codec;
+
+/*
+ * A product with one coded operand, W a fixed-width CodedMatrix<i8, Bd, C>
+ * (crates/uor-matmul-codec/src/matrix.rs:36-75, at :202-207) of w_rows x
+ * w_cols over `codec`, its codes row-major (w_rows * w_cols / MAX_BLOCK codes
+ * of code_bits / 8 bytes, 1 byte when packed):
+ *
+ *   transposed = 1: gemm_tabulated over TabulatedTriple (tabulated.rs:
+ *                   624-650, 2555): W is n x k, C := enc(alpha * A W^T + beta C)
+ *   transposed = 0: coded_gemm over CodedTriple (coded.rs:50-78, 98-140):
+ *                   W is k x n, C := enc(alpha * A W + beta C)
+ *
+ * A: m x k int8 view; c: m x n view of out_type elements; Linear epilogue and
+ * encode as gemm_i8.  A codes_len or shape that CodedMatrix::new refuses
+ * (MAX_BLOCK = 0, w_cols % MAX_BLOCK != 0, wrong code count) is status 3; then
+ * Nonconformant / OutputAliasesItself as the triples report them.  With an
+ * offer of uor_gfx950_suggested_scratch_coded bytes, W is decoded once into
+ * the scratch as a k x n int8 matrix and the dense int8 route runs (the
+ * decode-then-multiply spelling of the same value, CD-13); with less, a
+ * per-cell loop.  The bytes are the same.
+ */
+int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, const void *codes,
+                          uint64_t codes_len, uint64_t w_rows, uint64_t w_cols,
+                          int transposed, const uor_view *c, int out_type, int64_t alpha,
+                          int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
+                          void *stream, uor_route *route);
+
+/* The offer that lets gemm_coded take the decode-then-dense route. */
+uint64_t uor_gfx950_suggested_scratch_coded(uint64_t m, uint64_t k, uint64_t n);
 
 /* =================================================== exact float GEMM */
 

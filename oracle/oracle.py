@@ -57,6 +57,9 @@ def lib():
         L.ora_gemm_trop.restype = _i32
         L.ora_gemm_trop_selected.argtypes = [_i32] + _VIEW * 4 + [_i32, _i64, _i32, _i64, _i32, _i32]
         L.ora_gemm_trop_selected.restype = _i32
+        L.ora_coded_decode.argtypes = [_i32, _i32, _i32, _i32, _i64, _u64, _u64, _vp, _u64,
+                                       _vp, _u64, _u64, _u64, _vp]
+        L.ora_coded_decode.restype = _i32
         _lib = L
     return _lib
 
@@ -196,3 +199,51 @@ def fast_gemm_i8_i32(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, row0=0, rows=
     rows = m if rows is None else rows
     return fast().fr_gemm_i8_i32(m, k, n, int(alpha), _ptr(a), lda, _ptr(b), ldb, int(beta),
                                  _ptr(c), ldc, row0, rows, threads, int(force_avx2))
+
+
+# ------------------------------------------------------------------- codecs
+TIER = {"identity": 0, "grid": 1, "book": 2, "sign": 3, "ternary": 4}
+
+
+def codec(tier, code_bits=16, packed=0, zero=None, table=None, entries=None, block=1):
+    """A fixed-width codec over the i8 alphabet (codecs.rs): the base tier,
+    its code width, Packed<_, P> when packed > 0, Offset<_, zero> when zero is
+    not None.  `table` is an int8 array (Grid: N entries, Book: N*BLK)."""
+    t = None if table is None else np.ascontiguousarray(table, dtype=np.int8)
+    if entries is None:
+        entries = 0 if t is None else (t.size if tier == "grid" else t.size // max(block, 1))
+    return {"tier": TIER[tier], "code_bits": code_bits, "packed": packed,
+            "has_zero": int(zero is not None), "zero": 0 if zero is None else int(zero),
+            "entries": entries, "block": block, "table": t}
+
+
+def coded_decode(cd, codes, rows, cols):
+    """CodedMatrix::new + every CodedMatrix::at, as (status, rows x cols int8)."""
+    out = np.zeros(rows * cols, np.int8)
+    t = cd["table"]
+    codes = np.ascontiguousarray(codes)
+    st = lib().ora_coded_decode(cd["tier"], cd["code_bits"], cd["packed"], cd["has_zero"],
+                                cd["zero"], cd["entries"], cd["block"],
+                                None if t is None or t.size == 0 else _ptr(t),
+                                0 if t is None else t.size, _ptr(codes), codes.size, rows, cols,
+                                _ptr(out))
+    return STATUS[st], out.reshape(rows, cols)
+
+
+def gemm_coded(a, a_shape, a_strides, cd, codes, w_rows, w_cols, transposed, c, c_shape,
+               c_strides, alpha=1, beta=0, encode="nearest", out_bytes=None):
+    """gemm_tabulated (transposed: W is n x k) or coded_gemm (W is k x n) over
+    a fixed-width codec: the decode (CodedMatrix::at), then driver::gemm over
+    the decoded operand -- the decode-then-multiply value (CD-13)."""
+    st, w = coded_decode(cd, codes, w_rows, w_cols)
+    if st != "ok":
+        return st
+    w = np.ascontiguousarray(w).reshape(-1)
+    if transposed:
+        b_shape, b_strides = (w_cols, w_rows), (1, w_cols)
+    else:
+        b_shape, b_strides = (w_rows, w_cols), (w_cols, 1)
+    if w.size == 0:
+        w = np.zeros(1, np.int8)
+    return gemm_int(a, a_shape, a_strides, w, b_shape, b_strides, c, c_shape, c_strides,
+                    alpha=alpha, beta=beta, encode=encode, out_bytes=out_bytes)

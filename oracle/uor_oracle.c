@@ -26,6 +26,13 @@
  *       even, overflow, gradual underflow).
  *   ora_gemm_trop                 -- the reference's committed CX-11 fixtures
  *       (oracles/tropical) and a NumPy broadcast max-plus.
+ *   ora_gemm_trop_selected        -- the reference's doc example (1+9 / 9+1
+ *       -> witness 0), CT-04/CT-05 cases, brute force with ties.
+ *   ora_coded_decode              -- the reference's codec known answers:
+ *       CK-03 (0x3A -> 2, -5; 0xE4 -> 0,1,2,3), CK-05 (Book = Identity =
+ *       Grid decodes), CK-01 (Offset = c - 8), and the exhaustive
+ *       cross-spellings CK-11 (Sign<8> = Packed<Grid<2>,8>) and CK-12
+ *       (Ternary<4> = Packed<Grid<4>,4>) over all 256 codes.
  *   Parity unpinned (documented, no independent witness): the i128 epilogue's
  *   saturating_mul-then-wrapping-add behaviour at |alpha*sum| >= 2^127, which
  *   no input of the GPU route can reach (|sum| < 2^63 there).
@@ -707,5 +714,115 @@ int ora_gemm_trop_selected(int elem_bytes,
             w[at(&W, i, j)] = idx < k ? idx : k;
         }
     }
+    return ORA_OK;
+}
+
+/* ------------------------------------------------------------------ codecs
+ * Codec<i8, Bd>::decode_element for the fixed-width tiers
+ * (crates/uor-matmul-codec/src/codecs.rs) and CodedMatrix::at
+ * (crates/uor-matmul-codec/src/matrix.rs:202-207).
+ */
+enum { TIER_IDENTITY = 0, TIER_GRID = 1, TIER_BOOK = 2, TIER_SIGN = 3, TIER_TERNARY = 4 };
+
+typedef struct {
+    int tier, code_bits, packed, has_zero;
+    int64_t zero;
+    uint64_t entries, block;
+    const int8_t *table;
+    uint64_t table_len;
+} ora_codec;
+
+/* MAX_BLOCK of the base tier: Identity and Grid decode one element per code
+ * (codecs.rs:46, 99); Book, Sign and Ternary BLK (:303, 384, 489). */
+static uint64_t codec_inner_block(const ora_codec *c) {
+    return (c->tier == TIER_IDENTITY || c->tier == TIER_GRID) ? 1 : c->block;
+}
+
+/* Packed: P * C::MAX_BLOCK (codecs.rs:177). */
+static uint64_t codec_max_block(const ora_codec *c) {
+    return (c->packed ? (uint64_t)c->packed : 1) * codec_inner_block(c);
+}
+
+static int8_t codec_base(const ora_codec *c, uint32_t code, uint64_t i) {
+    switch (c->tier) {
+    case TIER_IDENTITY: /* codecs.rs:49-51 */
+        return (int8_t)(uint8_t)code;
+    case TIER_GRID: /* codecs.rs:102-104 */
+        return c->table[code % c->entries];
+    case TIER_BOOK: /* codecs.rs:306-308 */
+        return c->table[(code % c->entries) * c->block + i % c->block];
+    case TIER_SIGN: { /* codecs.rs:387-400 */
+        uint64_t bit = i % c->block;
+        return (bit < (uint64_t)c->code_bits && ((code >> bit) & 1u)) ? 1 : -1;
+    }
+    default: { /* TIER_TERNARY, codecs.rs:492-516 */
+        uint64_t shift = 2 * (i % c->block);
+        uint32_t digit = shift < (uint64_t)c->code_bits ? (code >> shift) & 3u : 0u;
+        return digit == 0 ? -1 : digit == 2 ? 1 : 0;
+    }
+    }
+}
+
+static int8_t codec_decode(const ora_codec *c, uint32_t code, uint64_t i) {
+    int8_t v;
+    if (c->packed) {
+        /* Packed::decode_element (codecs.rs:181-199): the low sub-code first. */
+        uint32_t bits = 8u / (uint32_t)c->packed;
+        uint32_t mask = bits >= 8 ? 0xFFu : ((1u << bits) - 1u);
+        uint64_t ib = codec_inner_block(c);
+        uint64_t p = i / ib;
+        uint32_t sub = (code >> (bits * (uint32_t)p)) & mask;
+        v = codec_base(c, sub, i % ib);
+    } else {
+        v = codec_base(c, code, i);
+    }
+    /* Offset::decode_element (codecs.rs:608-616): i8 wrapping_sub. */
+    if (c->has_zero) v = (int8_t)(uint8_t)((uint32_t)(uint8_t)v - (uint32_t)(uint8_t)(int8_t)c->zero);
+    return v;
+}
+
+/* What the decode needs of a codec: a known tier, P dividing 8, code widths
+ * the tier's code type has, a table of N (x BLK) entries. */
+static int codec_check(const ora_codec *c) {
+    if (c->tier < TIER_IDENTITY || c->tier > TIER_TERNARY) return ORA_INVALID_ARGUMENT;
+    if (!(c->packed == 0 || c->packed == 1 || c->packed == 2 || c->packed == 4 || c->packed == 8))
+        return ORA_INVALID_ARGUMENT;
+    if (c->tier == TIER_IDENTITY && (c->packed || c->code_bits != 8)) return ORA_INVALID_ARGUMENT;
+    if (c->tier == TIER_GRID && c->code_bits != 16) return ORA_INVALID_ARGUMENT;
+    if (c->code_bits != 8 && c->code_bits != 16) return ORA_INVALID_ARGUMENT;
+    if (c->has_zero && (c->zero < -128 || c->zero > 127)) return ORA_INVALID_ARGUMENT;
+    if (c->tier == TIER_GRID || c->tier == TIER_BOOK) {
+        if (c->entries == 0) return ORA_INVALID_ARGUMENT;
+        uint64_t need = c->entries * (c->tier == TIER_BOOK ? c->block : 1);
+        if (c->tier == TIER_BOOK && c->block && need / c->block != c->entries) return ORA_INVALID_ARGUMENT;
+        if (!c->table || c->table_len < need) return ORA_SHORT_BUFFER;
+    }
+    /* The GPU cursor keeps positions inside a block in 32 bits; the oracle
+     * refuses the same codecs so both name one status. */
+    if (c->tier >= TIER_BOOK && c->block >= (1ull << 31)) return ORA_INVALID_ARGUMENT;
+    return ORA_OK;
+}
+
+/* CodedMatrix::new for a fixed-width tier (matrix.rs:36-55) and the decode of
+ * every element, row-major into out (rows x cols). */
+int ora_coded_decode(int tier, int code_bits, int packed, int has_zero, int64_t zero,
+                     uint64_t entries, uint64_t block, const int8_t *table, uint64_t table_len,
+                     const void *codes, uint64_t codes_len, uint64_t rows, uint64_t cols,
+                     int8_t *out) {
+    ora_codec c = {tier, code_bits, packed, has_zero, zero, entries, block, table, table_len};
+    int st = codec_check(&c);
+    if (st) return st;
+    uint64_t mb = codec_max_block(&c);
+    if (mb == 0 || cols % mb != 0) return ORA_SHORT_BUFFER;
+    uint64_t per_row = cols / mb;
+    if (per_row && rows > UINT64_MAX / per_row) return ORA_SHORT_BUFFER;
+    if (rows * per_row != codes_len) return ORA_SHORT_BUFFER;
+    int cb = packed ? 1 : code_bits / 8;
+    for (uint64_t r = 0; r < rows; r++)
+        for (uint64_t q = 0; q < cols; q++) {
+            uint64_t at = r * per_row + q / mb;
+            uint32_t code = cb == 1 ? ((const uint8_t *)codes)[at] : ((const uint16_t *)codes)[at];
+            out[r * cols + q] = codec_decode(&c, code, q % mb);
+        }
     return ORA_OK;
 }

@@ -1,0 +1,178 @@
+"""GPU parity of products with one coded operand (uor_gfx950_gemm_coded, through
+the C ABI) against the oracle (oracle/uor_oracle.c ora_coded_decode, then
+ora_gemm_int over the decoded operand -- the decode-then-multiply value the
+reference's CD-13 names).
+
+Every fixed-width tier over the i8 alphabet -- Identity, Grid<N> (power of two
+and not, past u16), Book<N,BLK,K>, Sign<BLK,K>, Ternary<BLK,K>, inside Packed<_,
+P> and Offset<_, zero> -- in both orientations (gemm_tabulated: W n x k;
+coded_gemm: W k x n), both routes (decode into the scratch then the dense int8
+route; no offer: the per-cell loop), output widths, alpha/beta, the
+CodedMatrix/triple statuses, and the 4-bit codec against gemm_lut4.
+
+Bar: bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+OUTDT = {"i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64}
+
+I4 = np.arange(16, dtype=np.int8) - 8
+
+SPECS = {
+    "identity": dict(tier="identity", code_bits=8),
+    "packed_grid16_p2": dict(tier="grid", packed=2, table=I4),
+    "packed_grid4_p4": dict(tier="grid", packed=4, table=np.array([-1, 0, 1, 0], np.int8)),
+    "grid300": dict(tier="grid", table=(np.arange(300) % 251 - 125).astype(np.int8)),
+    "grid70000": dict(tier="grid", table=((np.arange(70000) * 7) % 255 - 127).astype(np.int8)),
+    "book256x8": dict(tier="book", block=8, table=((np.arange(2048) * 13) % 256 - 128).astype(np.int8)),
+    "book64x3_u8": dict(tier="book", code_bits=8, block=3,
+                        table=((np.arange(192) * 5) % 256 - 128).astype(np.int8)),
+    "packed_book4x2_p2": dict(tier="book", code_bits=8, packed=2, block=2,
+                              table=np.array([10, 11, -20, 21, 30, -31, 40, 41], np.int8)),
+    "sign8": dict(tier="sign", block=8),
+    "sign8_u8": dict(tier="sign", code_bits=8, block=8),
+    "sign12_u8": dict(tier="sign", code_bits=8, block=12),
+    "sign16": dict(tier="sign", block=16),
+    "ternary4_u8": dict(tier="ternary", code_bits=8, block=4),
+    "ternary6_u8": dict(tier="ternary", code_bits=8, block=6),
+    "ternary8": dict(tier="ternary", block=8),
+    "packed_sign2_p4": dict(tier="sign", code_bits=8, packed=4, block=2),
+    "offset_grid16": dict(tier="grid", table=np.arange(16, dtype=np.int8), zero=8),
+    "offset_packed_grid16": dict(tier="grid", packed=2, table=np.arange(16, dtype=np.int8),
+                                 zero=-3),
+    "offset_ternary_wraps": dict(tier="ternary", code_bits=8, block=4, zero=-128),
+}
+
+
+def max_block(spec):
+    ib = spec.get("block", 1) if spec["tier"] in ("book", "sign", "ternary") else 1
+    return (spec.get("packed") or 1) * ib
+
+
+def run(oracle, uor, dev, spec, m, k, n, transposed, offer, out="i32", alpha=1, beta=0,
+        encode="nearest", seed=0, codes_len_delta=0, c_strides=None):
+    rng = np.random.default_rng(seed)
+    rows, cols = (n, k) if transposed else (k, n)
+    mb = max_block(spec)
+    ncodes = rows * cols // mb + codes_len_delta
+    wide = not spec.get("packed") and spec.get("code_bits", 16) == 16
+    codes = rng.integers(0, 1 << 16 if wide else 1 << 8, max(ncodes, 0)).astype(
+        np.uint16 if wide else np.uint8)
+    a = rng.integers(-128, 128, max(m * k, 1)).astype(np.int8)
+    cs = c_strides or (n, 1)
+    clen = max(1 + (m - 1) * abs(cs[0]) + (n - 1) * abs(cs[1]), 1) if m and n else 1
+    c0 = rng.integers(-1000, 1000, clen).astype(OUTDT[out])
+    kw = {x: spec[x] for x in ("code_bits", "packed", "zero", "block") if x in spec}
+    table = spec.get("table")
+    ocd = oracle.codec(spec["tier"], table=table, **kw)
+    want = c0.copy()
+    st = oracle.gemm_coded(a, (m, k), (k, 1), ocd, codes, rows, cols, transposed, want, (m, n),
+                           cs, alpha=alpha, beta=beta, encode=encode)
+    gtable = None if table is None else torch.from_numpy(table).to(dev)
+    gcd = uor.codec(spec["tier"], table=gtable, **kw)
+    gcodes = torch.from_numpy(codes.view(np.int16) if wide else codes).to(dev)
+    gc = torch.from_numpy(c0.copy()).to(dev)
+    scratch = None
+    if offer:
+        nb = uor.suggested_scratch_coded(m, k, n)
+        scratch = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
+    gst, route = uor.gemm_coded(torch.from_numpy(a).to(dev), (m, k), (k, 1), gcd, gcodes, rows,
+                                cols, transposed, gc, (m, n), cs, out=out, alpha=alpha,
+                                beta=beta, encode=encode, scratch=scratch)
+    torch.cuda.synchronize()
+    assert uor.STATUS.get(gst, gst) == st, (gst, st, route)
+    assert np.array_equal(gc.cpu().numpy(), want), (spec, m, k, n, transposed, route)
+    return st, route
+
+
+@pytest.mark.parametrize("name", sorted(SPECS))
+@pytest.mark.parametrize("transposed", [True, False])
+@pytest.mark.parametrize("offer", [True, False])
+def test_tiers_against_oracle(oracle, uor, dev, name, transposed, offer):
+    """k and n multiples of 48 (every MAX_BLOCK here divides 48)."""
+    m, k, n = 5, 96, 48
+    st, route = run(oracle, uor, dev, SPECS[name], m, k, n, transposed, offer, alpha=3, beta=-2,
+                    seed=len(name))
+    assert st == "ok"
+    assert route["kind"] == ("coded_dense" if offer else "coded_direct"), route
+
+
+@pytest.mark.parametrize("name", ["packed_grid16_p2", "sign8", "ternary4_u8", "book256x8",
+                                  "offset_packed_grid16"])
+@pytest.mark.parametrize("transposed", [True, False])
+def test_larger_shapes_dense_route(oracle, uor, dev, name, transposed):
+    """Ragged tiles on both edges of the decode (n, k not multiples of 128)
+    and a dense route of several tiles."""
+    m, k, n = 130, 432, 288
+    st, route = run(oracle, uor, dev, SPECS[name], m, k, n, transposed, True, seed=7)
+    assert st == "ok" and route["kind"] == "coded_dense", route
+
+
+@pytest.mark.parametrize("out", ["i8", "i16", "i32", "i64"])
+@pytest.mark.parametrize("encode", ["nearest", "wrapping"])
+@pytest.mark.parametrize("offer", [True, False])
+def test_outputs_and_encodes(oracle, uor, dev, out, encode, offer):
+    for alpha, beta in [(1, 0), (7, -3), (1 << 40, 5)]:
+        run(oracle, uor, dev, SPECS["ternary8"], 9, 48, 96, True, offer, out=out, alpha=alpha,
+            beta=beta, encode=encode, seed=3)
+
+
+def test_strided_output_and_empty(oracle, uor, dev):
+    spec = SPECS["sign8"]
+    run(oracle, uor, dev, spec, 6, 48, 16, True, True, c_strides=(1, 6))      # column-major C
+    run(oracle, uor, dev, spec, 6, 48, 16, False, False, c_strides=(-16, 1))  # reversed rows
+    st, route = run(oracle, uor, dev, spec, 6, 0, 16, True, True, alpha=2, beta=-1)  # k = 0
+    assert st == "ok" and route["kind"] == "epilogue_only", route
+    run(oracle, uor, dev, spec, 0, 48, 16, True, True)                        # m = 0
+
+
+def test_statuses(oracle, uor, dev):
+    spec = SPECS["ternary4_u8"]
+    # a code count CodedMatrix::new refuses
+    st, _ = run(oracle, uor, dev, spec, 4, 48, 16, True, True, codes_len_delta=1)
+    assert st == "short_buffer"
+    st, _ = run(oracle, uor, dev, spec, 4, 48, 16, False, False, codes_len_delta=-1)
+    assert st == "short_buffer"
+    # a width that is not a multiple of MAX_BLOCK (k = 50 along W's rows)
+    st, _ = run(oracle, uor, dev, spec, 4, 50, 16, True, True)
+    assert st == "short_buffer"
+    # an aliasing output
+    st, _ = run(oracle, uor, dev, spec, 4, 48, 16, True, True, c_strides=(0, 1))
+    assert st == "output_aliases_itself"
+    # nonconformant: A's depth differs from W's
+    a = torch.zeros(4 * 40, dtype=torch.int8, device=dev)
+    codes = torch.zeros(16 * 48 // 4, dtype=torch.uint8, device=dev)
+    c = torch.zeros(4 * 16, dtype=torch.int32, device=dev)
+    gst, _ = uor.gemm_coded(a, (4, 40), (40, 1), uor.codec("ternary", code_bits=8, block=4),
+                            codes, 16, 48, True, c, (4, 16), (16, 1))
+    assert uor.STATUS[gst] == "nonconformant"
+    # a tier the library does not know, and P not dividing 8
+    for bad in (uor.codec(9, code_bits=8), uor.codec("sign", code_bits=8, packed=3, block=2)):
+        gst, _ = uor.gemm_coded(a, (4, 40), (40, 1), bad, codes, 16, 48, True, c, (4, 16),
+                                (16, 1))
+        assert uor.STATUS[gst] == "invalid_argument"
+
+
+def test_four_bit_codec_equals_lut4(uor, dev):
+    """Packed<Grid<16>,2> through gemm_coded (one codebook) and through
+    gemm_lut4 (group = n): the same bytes."""
+    rng = np.random.default_rng(9)
+    m, k, n = 33, 512, 200
+    a = torch.from_numpy(rng.integers(-128, 128, m * k).astype(np.int8)).to(dev)
+    codes = torch.from_numpy(rng.integers(0, 256, n * k // 2).astype(np.uint8)).to(dev)
+    book = torch.from_numpy((rng.integers(-128, 128, 16)).astype(np.int8)).to(dev)
+    c1 = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    c2 = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    for offer in (True, False):
+        nb = uor.suggested_scratch_coded(m, k, n) if offer else 0
+        scratch = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
+        st, _ = uor.gemm_coded(a, (m, k), (k, 1), uor.codec("grid", packed=2, table=book), codes,
+                               n, k, True, c1, (m, n), (n, 1), scratch=scratch)
+        assert st == 0
+        st, _ = uor.gemm_lut4(a, m, k, (k, 1), codes, n, book, n, c2, (n, 1))
+        assert st == 0
+        torch.cuda.synchronize()
+        assert torch.equal(c1, c2), offer

@@ -1,0 +1,372 @@
+// Products with one coded operand, any fixed-width codec tier over the i8
+// alphabet, on gfx950.
+//
+// Replaces gemm_tabulated (crates/uor-matmul-gemm/src/tabulated.rs:2555, W
+// n x k, transposed by declaration) and coded_gemm (crates/uor-matmul-gemm/
+// src/coded.rs:98-140, B k x n) for the tiers of crates/uor-matmul-codec/src/
+// codecs.rs: Identity, Grid<N>, Book<N,BLK,K>, Sign<BLK,K>, Ternary<BLK,K>,
+// each optionally inside Packed<_, P> and Offset<_, zero>.  The codec is not an
+// argument of the arithmetic (CK-05, CD-13): every element decodes to one i8
+// value and the product is the exact i8 product of the decoded operand.
+//
+// Routes.  With a scratch offer of k * round_up(n, 16) bytes (plus the dense
+// route's own), `coded_decode_kernel` writes the decoded operand once as a
+// k x n int8 matrix -- 128 x 128 tiles through LDS, 16-byte row stores -- and
+// the dense int8 MFMA route multiplies it.  Without an offer, one thread per
+// output cell decodes its column as it sums.  Both give the same bytes.
+
+#include "common.hpp"
+
+extern "C" int uor_gfx950_gemm_i8(const uor_view *a, const uor_view *b, const uor_view *c, int out_type,
+                                  int64_t alpha, int64_t beta, int encode, void *scratch,
+                                  uint64_t scratch_bytes, void *stream, uor_route *route);
+extern "C" uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n);
+
+namespace uor {
+
+// A codec as the decode reads it (see uor_codec).
+struct CodecDev {
+    int tier, code_bits, packed, has_zero;
+    int zero;                // Offset's zero point (i8)
+    uint32_t sub_bits, sub_mask;
+    uint64_t entries, block;
+    uint64_t ib, mb;         // the base tier's MAX_BLOCK, and the codec's
+    const int8_t *table;
+};
+
+// A coded operand: rows x cols over `cd`, codes row-major, `cb` bytes each.
+struct CodedArgs {
+    CodecDev cd;
+    const uint8_t *codes;
+    int cb;
+    uint64_t rows, cols, per_row;
+};
+
+// Codec<i8, Bd>::decode_element of the base tier (codecs.rs:49-51 Identity,
+// :102-104 Grid, :306-308 Book, :387-400 Sign, :492-516 Ternary).
+__device__ inline int dec_base(const CodecDev &c, uint32_t code, uint64_t i) {
+    switch (c.tier) {
+    case UOR_TIER_IDENTITY: return (int)(int8_t)(uint8_t)code;
+    case UOR_TIER_GRID: return c.table[code % c.entries];
+    case UOR_TIER_BOOK: return c.table[(code % c.entries) * c.block + i % c.block];
+    case UOR_TIER_SIGN: {
+        const uint64_t bit = i % c.block;
+        return (bit < (uint64_t)c.code_bits && ((code >> bit) & 1u)) ? 1 : -1;
+    }
+    default: {
+        const uint64_t shift = 2 * (i % c.block);
+        const uint32_t d = shift < (uint64_t)c.code_bits ? (code >> shift) & 3u : 0u;
+        return d == 0 ? -1 : (d == 2 ? 1 : 0);
+    }
+    }
+}
+
+// Packed (codecs.rs:181-199: the low sub-code first) and Offset
+// (codecs.rs:608-616: i8 wrapping_sub) around the base tier.
+__device__ inline int8_t dec(const CodecDev &c, uint32_t code, uint64_t i) {
+    int v;
+    if (c.packed) {
+        const uint64_t p = i / c.ib;
+        v = dec_base(c, (code >> (c.sub_bits * (uint32_t)p)) & c.sub_mask, i % c.ib);
+    } else {
+        v = dec_base(c, code, i);
+    }
+    if (c.has_zero) v -= c.zero;
+    return (int8_t)v;
+}
+
+// CodedMatrix::at for a fixed-width tier (matrix.rs:202-207).
+__device__ inline int8_t coded_at(const CodedArgs &W, uint64_t r, uint64_t q) {
+    const uint64_t at = r * W.per_row + q / W.cd.mb;
+    const uint32_t code = W.cb == 1 ? (uint32_t)W.codes[at] : (uint32_t)((const uint16_t *)W.codes)[at];
+    return dec(W.cd, code, q % W.cd.mb);
+}
+
+// A cursor along one row of a coded operand: the stored code, the sub-code
+// of a packed byte it is at, and the position inside the base tier's block,
+// advanced one element at a time without divisions.
+struct Walk {
+    uint64_t at;      // index of the stored code
+    uint32_t code;    // the stored code
+    uint32_t sub;     // the base tier's code (sub-code of a packed byte), % N for Grid/Book
+    uint32_t sp, ii;  // sub-code index in the byte, position in the base block
+};
+
+__device__ inline uint32_t load_code(const CodedArgs &W, uint64_t at) {
+    return W.cb == 1 ? (uint32_t)W.codes[at] : (uint32_t)((const uint16_t *)W.codes)[at];
+}
+
+__device__ inline void walk_sub(const CodedArgs &W, Walk &w) {
+    const CodecDev &c = W.cd;
+    uint32_t s = c.packed ? (w.code >> (c.sub_bits * w.sp)) & c.sub_mask : w.code;
+    if ((c.tier == UOR_TIER_GRID || c.tier == UOR_TIER_BOOK) && c.entries <= 0xFFFFu) s %= (uint32_t)c.entries;
+    w.sub = s;
+}
+
+// The cursor at element (r, q) of the operand.
+__device__ inline void walk_start(const CodedArgs &W, Walk &w, uint64_t r, uint64_t q) {
+    const uint32_t pos = (uint32_t)(q % W.cd.mb);
+    w.at = r * W.per_row + q / W.cd.mb;
+    w.sp = pos / (uint32_t)W.cd.ib;
+    w.ii = pos % (uint32_t)W.cd.ib;
+    w.code = load_code(W, w.at);
+    walk_sub(W, w);
+}
+
+// The element under the cursor (dec, with the cursor's state).
+__device__ inline int8_t walk_value(const CodedArgs &W, const Walk &w) {
+    const CodecDev &c = W.cd;
+    int v;
+    switch (c.tier) {
+    case UOR_TIER_IDENTITY: v = (int)(int8_t)(uint8_t)w.sub; break;
+    case UOR_TIER_GRID: v = c.table[w.sub]; break;
+    case UOR_TIER_BOOK: v = c.table[(uint64_t)w.sub * c.block + w.ii]; break;
+    case UOR_TIER_SIGN: v = (w.ii < (uint32_t)c.code_bits && ((w.sub >> w.ii) & 1u)) ? 1 : -1; break;
+    default: {
+        const uint32_t sh = 2 * w.ii;
+        const uint32_t d = sh < (uint32_t)c.code_bits ? (w.sub >> sh) & 3u : 0u;
+        v = d == 0 ? -1 : (d == 2 ? 1 : 0);
+    }
+    }
+    if (c.has_zero) v -= c.zero;
+    return (int8_t)v;
+}
+
+// Advance by one element; `more` says whether another element follows in
+// this row (so no code past the row's last is read).
+__device__ inline void walk_next(const CodedArgs &W, Walk &w, bool more) {
+    if (++w.ii < (uint32_t)W.cd.ib) return;
+    w.ii = 0;
+    if (W.cd.packed && ++w.sp < (uint32_t)W.cd.packed) {
+        walk_sub(W, w);
+        return;
+    }
+    w.sp = 0;
+    ++w.at;
+    if (more) {
+        w.code = load_code(W, w.at);
+        walk_sub(W, w);
+    }
+}
+
+// The decoded operand as a k x n int8 matrix (row stride ldw, a multiple of
+// 16).  W n x k (tabulated): one 128 x 128 tile per workgroup; each thread
+// walks 64 consecutive elements of one row of W (one column of the tile) into
+// LDS, then the tile leaves as 16-byte row chunks.
+__global__ void __launch_bounds__(256) coded_decode_t_kernel(CodedArgs W, uint64_t k, uint64_t n, int8_t *out,
+                                                             uint64_t ldw) {
+    __shared__ __attribute__((aligned(16))) int8_t tile[128][128];
+    const int t = threadIdx.x;
+    const uint64_t j0 = (uint64_t)blockIdx.x * 128, k0 = (uint64_t)blockIdx.y * 128;
+    const int cl = t & 127, kh = t >> 7;
+    const uint64_t j = j0 + cl, p0 = k0 + 64 * kh;
+    if (j < n && p0 < k) {
+        const int cnt = (int)(k - p0 < 64 ? k - p0 : 64);
+        Walk w;
+        walk_start(W, w, j, p0);
+        for (int q = 0; q < cnt; ++q) {
+            tile[64 * kh + q][cl] = walk_value(W, w);
+            walk_next(W, w, q + 1 < cnt);
+        }
+    }
+    __syncthreads();
+    const int ch = t & 7;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int r = pass * 32 + (t >> 3);
+        const uint64_t kk = k0 + r, jc = j0 + 16 * ch;
+        if (kk < k && jc < ldw) *(uint4 *)(out + kk * ldw + jc) = *(const uint4 *)&tile[r][16 * ch];
+    }
+}
+
+// W k x n (coded_gemm): the rows are already the output's; each thread walks
+// 16 consecutive elements of one row and stores them as one 16-byte chunk
+// (zeros past column n, inside the row stride).
+__global__ void __launch_bounds__(256) coded_decode_kernel(CodedArgs W, uint64_t k, uint64_t n, int8_t *out,
+                                                           uint64_t ldw) {
+    const uint64_t chunks = ldw / 16;
+    const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= k * chunks) return;
+    const uint64_t p = id / chunks, j0 = 16 * (id % chunks);
+    union {
+        uint4 v;
+        int8_t b[16];
+    } u;
+    u.v = uint4{0, 0, 0, 0};
+    if (j0 < n) {
+        const int cnt = (int)(n - j0 < 16 ? n - j0 : 16);
+        Walk w;
+        walk_start(W, w, p, j0);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            if (q < cnt) {
+                u.b[q] = walk_value(W, w);
+                walk_next(W, w, q + 1 < cnt);
+            }
+        }
+    }
+    *(uint4 *)(out + p * ldw + j0) = u.v;
+}
+
+struct DirectArgs {
+    const int8_t *a;
+    int64_t ars, acs;
+    char *c;
+    int64_t crs, ccs;
+    uint64_t m, k, n;
+    int64_t alpha, beta;
+    int mode;
+};
+
+// No offer: one thread per cell, its column of W decoded as it is summed
+// (coded.rs:120-131's walk), then Linear::finish.
+template <bool TRANS, int OB>
+__global__ void __launch_bounds__(256) coded_direct_kernel(CodedArgs W, DirectArgs D) {
+    const uint64_t cell = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (cell >= D.m * D.n) return;
+    const uint64_t i = cell / D.n, j = cell % D.n;
+    int64_t sum = 0;
+    for (uint64_t p = 0; p < D.k; ++p) {
+        const int8_t w = TRANS ? coded_at(W, j, p) : coded_at(W, p, j);
+        sum += (int64_t)D.a[(int64_t)i * D.ars + (int64_t)p * D.acs] * w;
+    }
+    linear_finish<OB, false>(D.c + ((int64_t)i * D.crs + (int64_t)j * D.ccs) * OB, sum, D.alpha, D.beta,
+                             D.mode);
+}
+
+template <bool TRANS>
+static void launch_direct(const CodedArgs &W, const DirectArgs &D, int ob, dim3 grid, hipStream_t s) {
+    switch (ob) {
+    case 1: hipLaunchKernelGGL((coded_direct_kernel<TRANS, 1>), grid, dim3(256), 0, s, W, D); break;
+    case 2: hipLaunchKernelGGL((coded_direct_kernel<TRANS, 2>), grid, dim3(256), 0, s, W, D); break;
+    case 4: hipLaunchKernelGGL((coded_direct_kernel<TRANS, 4>), grid, dim3(256), 0, s, W, D); break;
+    case 8: hipLaunchKernelGGL((coded_direct_kernel<TRANS, 8>), grid, dim3(256), 0, s, W, D); break;
+    default: hipLaunchKernelGGL((coded_direct_kernel<TRANS, 16>), grid, dim3(256), 0, s, W, D); break;
+    }
+}
+
+static uint64_t round_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+
+// The decoded operand's bytes in the scratch (k x round_up(n, 16), 256-byte
+// aligned end).
+static uint64_t decoded_bytes(uint64_t k, uint64_t n) { return round_up(k * round_up(n, 16), 256); }
+
+// What the decode needs of a codec (the constructors' own bound checks are
+// the caller's): a known tier, P dividing 8, the tier's code widths, a table
+// of N (x BLK) entries.
+static int codec_dev(const uor_codec *c, CodecDev *d) {
+    if (!c) return UOR_INVALID_ARGUMENT;
+    if (c->tier < UOR_TIER_IDENTITY || c->tier > UOR_TIER_TERNARY) return UOR_INVALID_ARGUMENT;
+    if (!(c->packed == 0 || c->packed == 1 || c->packed == 2 || c->packed == 4 || c->packed == 8))
+        return UOR_INVALID_ARGUMENT;
+    if (c->tier == UOR_TIER_IDENTITY && (c->packed || c->code_bits != 8)) return UOR_INVALID_ARGUMENT;
+    if (c->tier == UOR_TIER_GRID && c->code_bits != 16) return UOR_INVALID_ARGUMENT;
+    if (c->code_bits != 8 && c->code_bits != 16) return UOR_INVALID_ARGUMENT;
+    if (c->has_zero && (c->zero < -128 || c->zero > 127)) return UOR_INVALID_ARGUMENT;
+    if (c->tier == UOR_TIER_GRID || c->tier == UOR_TIER_BOOK) {
+        if (c->entries == 0) return UOR_INVALID_ARGUMENT;
+        uint64_t need = c->entries;
+        if (c->tier == UOR_TIER_BOOK && __builtin_mul_overflow(c->entries, c->block, &need))
+            return UOR_INVALID_ARGUMENT;
+        if (!c->table || c->table_len < need) return UOR_SHORT_BUFFER;
+    }
+    // The cursor keeps positions inside a block in 32 bits.
+    if (c->tier >= UOR_TIER_BOOK && c->block >= (1ull << 31)) return UOR_INVALID_ARGUMENT;
+    d->tier = c->tier;
+    d->code_bits = c->code_bits;
+    d->packed = c->packed;
+    d->has_zero = c->has_zero != 0;
+    d->zero = (int)c->zero;
+    d->sub_bits = c->packed ? 8u / (uint32_t)c->packed : 8u;
+    d->sub_mask = d->sub_bits >= 8 ? 0xFFu : ((1u << d->sub_bits) - 1u);
+    d->entries = c->entries;
+    d->block = c->block;
+    d->ib = (c->tier == UOR_TIER_IDENTITY || c->tier == UOR_TIER_GRID) ? 1 : c->block;
+    if (__builtin_mul_overflow(d->ib, (uint64_t)(c->packed ? c->packed : 1), &d->mb)) return UOR_SHORT_BUFFER;
+    d->table = c->table;
+    return UOR_OK;
+}
+
+}  // namespace uor
+
+using namespace uor;
+
+extern "C" uint64_t uor_gfx950_suggested_scratch_coded(uint64_t m, uint64_t k, uint64_t n) {
+    if (m == 0 || n == 0 || k == 0) return 0;
+    return decoded_bytes(k, n) + uor_gfx950_suggested_scratch_i8(m, k, n);
+}
+
+extern "C" int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, const void *codes,
+                                     uint64_t codes_len, uint64_t w_rows, uint64_t w_cols, int transposed,
+                                     const uor_view *c, int out_type, int64_t alpha, int64_t beta, int encode,
+                                     void *scratch, uint64_t scratch_bytes, void *stream, uor_route *route) {
+    route_set(route, UOR_ROUTE_NONE);
+    if (!valid_out_type(out_type) || !valid_encode(encode)) return UOR_INVALID_ARGUMENT;
+    CodedArgs W{};
+    int st = codec_dev(codec, &W.cd);
+    if (st) return st;
+    // CodedMatrix::new for a fixed-width tier (matrix.rs:36-55).
+    if (W.cd.mb == 0 || w_cols % W.cd.mb != 0) return UOR_SHORT_BUFFER;
+    W.per_row = w_cols / W.cd.mb;
+    uint64_t ncodes;
+    if (__builtin_mul_overflow(w_rows, W.per_row, &ncodes) || ncodes != codes_len) return UOR_SHORT_BUFFER;
+    if (ncodes != 0 && codes == nullptr) return UOR_SHORT_BUFFER;
+    W.codes = (const uint8_t *)codes;
+    W.cb = codec->packed ? 1 : codec->code_bits / 8;
+    W.rows = w_rows;
+    W.cols = w_cols;
+    // MatView::new for A and C, then TabulatedTriple::new (tabulated.rs:
+    // 624-650) or CodedTriple::new (coded.rs:50-78).
+    Placed A, C;
+    if ((st = place(a, 1, &A))) return st;
+    if ((st = place(c, out_type, &C))) return st;
+    const uint64_t k = transposed ? w_cols : w_rows, n = transposed ? w_rows : w_cols;
+    if (A.cols != k || C.rows != A.rows || C.cols != n) return UOR_NONCONFORMANT;
+    if (self_aliases(C.rows, C.cols, C.rs, C.cs)) return UOR_OUTPUT_ALIASES_ITSELF;
+    if (C.rows == 0 || C.cols == 0) return UOR_OK;
+    if (W.cb == 2 && ((uintptr_t)codes & 1)) return UOR_INVALID_ARGUMENT;
+    if ((uintptr_t)C.base % (uint64_t)(out_type > 8 ? 8 : out_type)) return UOR_INVALID_ARGUMENT;
+    const uint64_t m = A.rows;
+    hipStream_t s = (hipStream_t)stream;
+
+    const uint64_t wbytes = k ? decoded_bytes(k, n) : 0;
+    const bool dense = k > 0 && scratch && scratch_bytes >= wbytes + uor_gfx950_suggested_scratch_i8(m, k, n) &&
+                       (n + 127) / 128 <= 0x7FFFFFFFull && (k + 127) / 128 <= 65535ull &&
+                       (k * (round_up(n, 16) / 16) + 255) / 256 <= 0x7FFFFFFFull;
+    if (dense) {
+        const uint64_t ldw = round_up(n, 16);
+        int8_t *wt = (int8_t *)scratch;
+        if (transposed) {
+            const dim3 grid((unsigned)((n + 127) / 128), (unsigned)((k + 127) / 128));
+            hipLaunchKernelGGL(coded_decode_t_kernel, grid, dim3(256), 0, s, W, k, n, wt, ldw);
+        } else {
+            const uint64_t blocks = (k * (ldw / 16) + 255) / 256;
+            hipLaunchKernelGGL(coded_decode_kernel, dim3((unsigned)blocks), dim3(256), 0, s, W, k, n, wt, ldw);
+        }
+        UOR_HIP(hipGetLastError());
+        const uor_view bv{wt, k * ldw, k, n, (int64_t)ldw, 1};
+        const int st2 = uor_gfx950_gemm_i8(a, &bv, c, out_type, alpha, beta, encode, (char *)scratch + wbytes,
+                                           scratch_bytes - wbytes, stream, route);
+        if (route && st2 == UOR_OK) {
+            route->kind = UOR_ROUTE_CODED_DENSE;
+            route->launches += 1;
+            route->scratch_used += wbytes;
+        }
+        return st2;
+    }
+    {
+        const uint64_t cells = m * n, blocks = (cells + 255) / 256;
+        if (cells / n != m || blocks > 0x7FFFFFFFull) return UOR_INVALID_ARGUMENT;
+        DirectArgs D{(const int8_t *)A.base, A.rs, A.cs, C.base, C.rs, C.cs, m, k, n, alpha, beta, encode};
+        if (route) {
+            route->kind = k ? UOR_ROUTE_CODED_DIRECT : UOR_ROUTE_EPILOGUE_ONLY;
+            route->tile_m = route->tile_n = route->tile_k = 1;
+            route->split_k = 1;
+            route->launches = 1;
+        }
+        if (transposed) launch_direct<true>(W, D, out_type, dim3((unsigned)blocks), s);
+        else launch_direct<false>(W, D, out_type, dim3((unsigned)blocks), s);
+        UOR_HIP(hipGetLastError());
+    }
+    return UOR_OK;
+}

@@ -22,7 +22,8 @@ ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
           4: "invalid_argument"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
-          10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
+          10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill",
+          13: "coded_dense", 14: "coded_direct", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
           31: "trop_selected", 32: "trop_selected_direct", 40: "int_crt", 41: "int_direct"}
 WITNESS = {"lexicographic": 0, "compare_pass": 1}
 
@@ -37,6 +38,8 @@ SYMBOLS = [
     "uor_gfx950_suggested_scratch_int",
     "uor_gfx950_gemm_lut4",
     "uor_gfx950_suggested_scratch_lut4",
+    "uor_gfx950_gemm_coded",
+    "uor_gfx950_suggested_scratch_coded",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
     "uor_gfx950_sgemm",
@@ -50,6 +53,17 @@ SYMBOLS = [
 class View(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("len", ctypes.c_uint64), ("rows", ctypes.c_uint64),
                 ("cols", ctypes.c_uint64), ("rs", ctypes.c_int64), ("cs", ctypes.c_int64)]
+
+
+class Codec(ctypes.Structure):
+    _fields_ = [("tier", ctypes.c_int32), ("code_bits", ctypes.c_int32),
+                ("packed", ctypes.c_int32), ("has_zero", ctypes.c_int32),
+                ("zero", ctypes.c_int64), ("entries", ctypes.c_uint64),
+                ("block", ctypes.c_uint64), ("table", ctypes.c_void_p),
+                ("table_len", ctypes.c_uint64)]
+
+
+TIER = {"identity": 0, "grid": 1, "book": 2, "sign": 3, "ternary": 4}
 
 
 class Route(ctypes.Structure):
@@ -110,6 +124,13 @@ def lib():
             L.uor_gfx950_gemm_lut4.restype = _i32
             L.uor_gfx950_suggested_scratch_lut4.argtypes = [_u64, _u64, _u64]
             L.uor_gfx950_suggested_scratch_lut4.restype = _u64
+        if hasattr(L, "uor_gfx950_gemm_coded"):
+            L.uor_gfx950_gemm_coded.argtypes = [_PV, ctypes.POINTER(Codec), _vp, _u64, _u64, _u64,
+                                                _i32, _PV, _i32, _i64, _i64, _i32, _vp, _u64, _vp,
+                                                _PR]
+            L.uor_gfx950_gemm_coded.restype = _i32
+            L.uor_gfx950_suggested_scratch_coded.argtypes = [_u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_coded.restype = _u64
         if hasattr(L, "uor_gfx950_gemm_float"):
             L.uor_gfx950_gemm_float.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32, _vp, _u64,
                                                 _vp, _PR]
@@ -308,3 +329,38 @@ def gemm_trop_i8_selected(a, a_shape, a_strides, b, b_shape, b_strides, c, c_sha
         0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
         ctypes.byref(r))
     return st, r.as_dict()
+
+
+def codec(tier, code_bits=16, packed=0, zero=None, table=None, entries=None, block=1):
+    """A uor_codec: the base tier (identity/grid/book/sign/ternary), its code
+    width in bits, Packed<_, P> when packed > 0, Offset<_, zero> when zero is
+    not None.  `table` is an int8 device tensor (Grid: N entries, Book: N*BLK);
+    keep it alive for the call."""
+    n = 0 if table is None else table.numel()
+    if entries is None:
+        entries = n if tier == "grid" else (n // max(block, 1) if tier == "book" else 0)
+    return Codec(TIER.get(tier, tier), code_bits, packed, int(zero is not None),
+                 0 if zero is None else int(zero), entries, block, _ptr(table), n)
+
+
+def gemm_coded(a, a_shape, a_strides, cd, codes, w_rows, w_cols, transposed, c, c_shape,
+               c_strides, out="i32", alpha=1, beta=0, encode="nearest", scratch=None,
+               stream=None):
+    """gemm_tabulated (transposed: W is n x k) or coded_gemm (W is k x n) with
+    W a fixed-width coded operand: `codes` is a device tensor of the stored
+    codes (uint8, or int16/uint16 for 16-bit codes)."""
+    ob = OUT[out]
+    rec = 2 if ob == 16 else 1
+    av = view(a, *a_shape, *a_strides)
+    cv = view(c, *c_shape, *c_strides, rec=rec)
+    r = Route()
+    st = lib().uor_gfx950_gemm_coded(
+        ctypes.byref(av), ctypes.byref(cd), _ptr(codes), codes.numel(), w_rows, w_cols,
+        int(bool(transposed)), ctypes.byref(cv), ob, int(alpha), int(beta), ENCODE[encode],
+        _ptr(scratch), 0 if scratch is None else scratch.numel() * scratch.element_size(),
+        _stream(stream), ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def suggested_scratch_coded(m, k, n):
+    return lib().uor_gfx950_suggested_scratch_coded(m, k, n)
