@@ -88,6 +88,7 @@ typedef struct uor_view {
 #define UOR_ROUTE_LUT4_PREFILL 12 /* 4-bit table-lookup, many rows: decode W^T, dense int8 MFMA */
 #define UOR_ROUTE_CODED_DENSE 13  /* any fixed-width codec: decode W into scratch, dense int8 route */
 #define UOR_ROUTE_CODED_DIRECT 14 /* any fixed-width codec, no offer: per-cell decode and sum */
+#define UOR_ROUTE_CODED_GEMV 15   /* any fixed-width codec, W n x k, m <= 8: decode in registers, one wave per column */
 #define UOR_ROUTE_FLOAT_CRT 20    /* exact float: int8 residue MFMA + CRT */
 #define UOR_ROUTE_FLOAT_DIRECT 21 /* exact float: per-cell exact register */
 #define UOR_ROUTE_TROP_VALU 30    /* max-plus, packed i16 VALU */
@@ -258,9 +259,11 @@ typedef struct uor_codec {
  * A: m x k int8 view; c: m x n view of out_type elements; Linear epilogue and
  * encode as gemm_i8.  A codes_len or shape that CodedMatrix::new refuses
  * (MAX_BLOCK = 0, w_cols % MAX_BLOCK != 0, wrong code count) is status 3; then
- * Nonconformant / OutputAliasesItself as the triples report them.  With an
- * offer of uor_gfx950_suggested_scratch_coded bytes, W is decoded once into
- * the scratch as a k x n int8 matrix and the dense int8 route runs (the
+ * Nonconformant / OutputAliasesItself as the triples report them.  For
+ * transposed = 1, m <= 8 and k <= 2^22, the codes are decoded in registers as
+ * they are multiplied (no scratch).  Otherwise, with an offer of
+ * uor_gfx950_suggested_scratch_coded bytes, W is decoded once into the
+ * scratch as a k x n int8 matrix and the dense int8 route runs (the
  * decode-then-multiply spelling of the same value, CD-13); with less, a
  * per-cell loop.  The bytes are the same.
  */

@@ -91,13 +91,76 @@ def run(oracle, uor, dev, spec, m, k, n, transposed, offer, out="i32", alpha=1, 
 @pytest.mark.parametrize("name", sorted(SPECS))
 @pytest.mark.parametrize("transposed", [True, False])
 @pytest.mark.parametrize("offer", [True, False])
-def test_tiers_against_oracle(oracle, uor, dev, name, transposed, offer):
-    """k and n multiples of 48 (every MAX_BLOCK here divides 48)."""
-    m, k, n = 5, 96, 48
+@pytest.mark.parametrize("m", [5, 9])
+def test_tiers_against_oracle(oracle, uor, dev, name, transposed, offer, m):
+    """k and n multiples of 48 (every MAX_BLOCK here divides 48).  W n x k
+    with m <= 8 decodes in registers whatever the offer."""
+    k, n = 96, 48
     st, route = run(oracle, uor, dev, SPECS[name], m, k, n, transposed, offer, alpha=3, beta=-2,
-                    seed=len(name))
+                    seed=len(name) + m)
     assert st == "ok"
-    assert route["kind"] == ("coded_dense" if offer else "coded_direct"), route
+    want = ("coded_gemv" if transposed and m <= 8 else
+            "coded_dense" if offer else "coded_direct")
+    assert route["kind"] == want, route
+
+
+@pytest.mark.parametrize("name", ["packed_grid16_p2", "sign12_u8", "ternary6_u8", "book64x3_u8",
+                                  "grid300", "offset_ternary_wraps"])
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+def test_few_rows_ragged_depth(oracle, uor, dev, name, m):
+    """The register-decode route: depths that leave lane slices ragged (k not
+    a multiple of 16 or of 64 x 16, and shorter than 64 lanes' worth) and a
+    depth of several thousand, 1 to 8 rows."""
+    mb = max_block(SPECS[name])
+    for k in (mb * 7, mb * 40, mb * 1000):
+        st, route = run(oracle, uor, dev, SPECS[name], m, k, 37, True, False, alpha=-2, beta=1,
+                        seed=k + m)
+        assert st == "ok" and route["kind"] == "coded_gemv", route
+
+
+@pytest.mark.parametrize("name", sorted(SPECS))
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_few_rows_code_windows(oracle, uor, dev, name, m):
+    """Rows of W that are whole 16-byte code windows: the windowed variant of
+    the register-decode route (one window per lane and step), and for
+    one-byte codes of 4 or 8 elements at m <= 4 its table variant; fewer
+    windows than lanes and several steps per row, n not a multiple of the 4
+    columns a wave takes."""
+    spec = SPECS[name]
+    mb = max_block(spec)
+    cb = 1 if spec.get("packed") or spec.get("code_bits", 16) == 8 else 2
+    for wins in (5, 150):
+        k = 16 * wins * mb // cb
+        st, route = run(oracle, uor, dev, spec, m, k, 37, True, False, alpha=3, beta=-1,
+                        seed=k + m + len(name))
+        assert st == "ok" and route["kind"] == "coded_gemv", route
+        a_vec = k % 16 == 0
+        win = a_vec and (16 // cb) * mb % 16 == 0
+        lut = win and cb == 1 and mb in (4, 8) and m <= 4
+        assert route["operand_modes"] == (3 if lut else 2 if win else 1 if a_vec else 0), route
+
+
+def test_few_rows_strided_a(oracle, uor, dev):
+    """A read element by element (column-major and padded rows) on the
+    register-decode route."""
+    rng = np.random.default_rng(4)
+    m, k, n = 3, 200, 40
+    spec = SPECS["ternary4_u8"]
+    codes = rng.integers(0, 256, n * k // 4).astype(np.uint8)
+    for a_str, alen in (((1, m), m * k), ((k + 5, 1), m * (k + 5))):
+        a = rng.integers(-128, 128, alen).astype(np.int8)
+        want = np.zeros(m * n, np.int32)
+        ocd = oracle.codec("ternary", code_bits=8, block=4)
+        assert oracle.gemm_coded(a, (m, k), a_str, ocd, codes, n, k, True, want, (m, n),
+                                 (n, 1)) == "ok"
+        gc = torch.zeros(m * n, dtype=torch.int32, device=dev)
+        st, route = uor.gemm_coded(torch.from_numpy(a).to(dev), (m, k), a_str,
+                                   uor.codec("ternary", code_bits=8, block=4),
+                                   torch.from_numpy(codes).to(dev), n, k, True, gc, (m, n),
+                                   (n, 1))
+        torch.cuda.synchronize()
+        assert st == 0 and route["kind"] == "coded_gemv" and route["operand_modes"] == 0, route
+        assert np.array_equal(gc.cpu().numpy(), want), a_str
 
 
 @pytest.mark.parametrize("name", ["packed_grid16_p2", "sign8", "ternary4_u8", "book256x8",
@@ -115,9 +178,10 @@ def test_larger_shapes_dense_route(oracle, uor, dev, name, transposed):
 @pytest.mark.parametrize("encode", ["nearest", "wrapping"])
 @pytest.mark.parametrize("offer", [True, False])
 def test_outputs_and_encodes(oracle, uor, dev, out, encode, offer):
-    for alpha, beta in [(1, 0), (7, -3), (1 << 40, 5)]:
-        run(oracle, uor, dev, SPECS["ternary8"], 9, 48, 96, True, offer, out=out, alpha=alpha,
-            beta=beta, encode=encode, seed=3)
+    for m in (4, 9):  # the register-decode route, then dense / per-cell
+        for alpha, beta in [(1, 0), (7, -3), (1 << 40, 5)]:
+            run(oracle, uor, dev, SPECS["ternary8"], m, 48, 96, True, offer, out=out, alpha=alpha,
+                beta=beta, encode=encode, seed=3)
 
 
 def test_strided_output_and_empty(oracle, uor, dev):
@@ -160,13 +224,13 @@ def test_four_bit_codec_equals_lut4(uor, dev):
     """Packed<Grid<16>,2> through gemm_coded (one codebook) and through
     gemm_lut4 (group = n): the same bytes."""
     rng = np.random.default_rng(9)
-    m, k, n = 33, 512, 200
-    a = torch.from_numpy(rng.integers(-128, 128, m * k).astype(np.int8)).to(dev)
-    codes = torch.from_numpy(rng.integers(0, 256, n * k // 2).astype(np.uint8)).to(dev)
-    book = torch.from_numpy((rng.integers(-128, 128, 16)).astype(np.int8)).to(dev)
-    c1 = torch.zeros(m * n, dtype=torch.int32, device=dev)
-    c2 = torch.zeros(m * n, dtype=torch.int32, device=dev)
-    for offer in (True, False):
+    for m, offer in ((33, True), (33, False), (1, False), (8, False)):
+        k, n = 512, 200
+        a = torch.from_numpy(rng.integers(-128, 128, m * k).astype(np.int8)).to(dev)
+        codes = torch.from_numpy(rng.integers(0, 256, n * k // 2).astype(np.uint8)).to(dev)
+        book = torch.from_numpy((rng.integers(-128, 128, 16)).astype(np.int8)).to(dev)
+        c1 = torch.zeros(m * n, dtype=torch.int32, device=dev)
+        c2 = torch.zeros(m * n, dtype=torch.int32, device=dev)
         nb = uor.suggested_scratch_coded(m, k, n) if offer else 0
         scratch = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
         st, _ = uor.gemm_coded(a, (m, k), (k, 1), uor.codec("grid", packed=2, table=book), codes,

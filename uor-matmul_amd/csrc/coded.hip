@@ -208,6 +208,300 @@ __global__ void __launch_bounds__(256) coded_decode_kernel(CodedArgs W, uint64_t
     *(uint4 *)(out + p * ldw + j0) = u.v;
 }
 
+// ------------------------------------------------------------ few rows --
+//
+// m <= 8 and W n x k (the table-lookup orientation): no decoded copy.  One
+// wave per output column j; lane l walks its 16-aligned slice of row j of W
+// (contiguous codes, so a wave reads one run of the row), decodes each
+// element in registers and multiplies it into up to MR rows of A (int32 per
+// lane: a slice is at most 2^16 elements), then the wave adds its lanes in
+// int64 and lane r finishes row r.  The tier is a template parameter, so the
+// per-element decode is a handful of VALU instructions.
+constexpr uint64_t GEMV_MAX_K = 1ull << 22;
+
+struct GemvArgs {
+    const int8_t *a;
+    int64_t ars, acs;
+    int a_vec;  // unit column stride, 16-byte aligned rows: 16-byte loads
+    char *c;
+    int64_t crs, ccs;
+    uint64_t m, k, n;
+    int64_t alpha, beta;
+    int mode, ob;
+};
+
+template <int TIER>
+__device__ inline int8_t walk_value_t(const CodedArgs &W, const Walk &w) {
+    const CodecDev &c = W.cd;
+    int v;
+    if constexpr (TIER == UOR_TIER_IDENTITY) v = (int)(int8_t)(uint8_t)w.sub;
+    else if constexpr (TIER == UOR_TIER_GRID) v = c.table[w.sub];
+    else if constexpr (TIER == UOR_TIER_BOOK) v = c.table[(uint64_t)w.sub * c.block + w.ii];
+    else if constexpr (TIER == UOR_TIER_SIGN) v = (w.ii < (uint32_t)c.code_bits && ((w.sub >> w.ii) & 1u)) ? 1 : -1;
+    else {
+        const uint32_t sh = 2 * w.ii;
+        const uint32_t d = sh < (uint32_t)c.code_bits ? (w.sub >> sh) & 3u : 0u;
+        v = d == 0 ? -1 : (d == 2 ? 1 : 0);
+    }
+    if (c.has_zero) v -= c.zero;
+    return (int8_t)v;
+}
+
+__device__ inline void finish_any(char *cp, int64_t sum, const GemvArgs &G) {
+    switch (G.ob) {
+    case 1: linear_finish<1, false>(cp, sum, G.alpha, G.beta, G.mode); break;
+    case 2: linear_finish<2, false>(cp, sum, G.alpha, G.beta, G.mode); break;
+    case 4: linear_finish<4, false>(cp, sum, G.alpha, G.beta, G.mode); break;
+    case 8: linear_finish<8, false>(cp, sum, G.alpha, G.beta, G.mode); break;
+    default: linear_finish<16, false>(cp, sum, G.alpha, G.beta, G.mode); break;
+    }
+}
+
+template <int TIER, int MR>
+__global__ void __launch_bounds__(256) coded_gemv_kernel(CodedArgs W, GemvArgs G) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t j = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (j >= G.n) return;  // whole waves
+    const uint64_t slice = ((G.k + 63) / 64 + 15) / 16 * 16;
+    const uint64_t p0 = (uint64_t)lane * slice;
+    const uint64_t p1 = p0 + slice < G.k ? p0 + slice : G.k;
+    int acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0;
+    if (p0 < p1) {
+        Walk w;
+        walk_start(W, w, j, p0);
+        for (uint64_t p = p0; p < p1; p += 16) {
+            const int cnt = (int)(p1 - p < 16 ? p1 - p : 16);
+            int8_t av[MR][16];
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                if ((uint64_t)r < G.m) {
+                    if (G.a_vec && cnt == 16) {
+                        *(uint4 *)av[r] = *(const uint4 *)(G.a + (int64_t)r * G.ars + (int64_t)p);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            av[r][e] = e < cnt ? G.a[(int64_t)r * G.ars + (int64_t)(p + e) * G.acs] : 0;
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) av[r][e] = 0;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                if (e < cnt) {
+                    const int wv = walk_value_t<TIER>(W, w);
+                    walk_next(W, w, p + e + 1 < p1);
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) acc[r] += (int)av[r][e] * wv;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        int64_t v = acc[r];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == r && (uint64_t)r < G.m)
+            finish_any(G.c + ((int64_t)r * G.crs + (int64_t)j * G.ccs) * G.ob, v, G);
+    }
+}
+
+// The same product when each row of W is a whole number of 16-byte code
+// windows and A's rows are 16-byte aligned (the common case): lane l of the
+// wave takes windows l, l + 64, ... of row j, so a wave step reads 1 KiB of
+// the row with one 16-byte load per lane, and the next step's window is
+// loaded before this one is decoded.  A window holds 16 / cb codes, i.e.
+// E = (16 / cb) * MAX_BLOCK elements, a multiple of 16 (the host checks).
+template <int TIER, int MR>
+__global__ void __launch_bounds__(256) coded_gemv_win_kernel(CodedArgs W, GemvArgs G) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t j = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (j >= G.n) return;  // whole waves
+    const CodecDev &c = W.cd;
+    const uint64_t row_bytes = W.per_row * (uint64_t)W.cb;
+    const uint64_t nwin = row_bytes / 16;
+    const uint8_t *row = W.codes + j * row_bytes;
+    const uint32_t cpw = 16u / (uint32_t)W.cb;             // codes per window
+    const uint64_t E = (uint64_t)cpw * c.mb;                // elements per window
+    const uint32_t P = c.packed ? (uint32_t)c.packed : 1u;
+    const uint32_t ib = (uint32_t)c.ib;
+    int acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0;
+    uint64_t wi = (uint64_t)lane;
+    uint4 nxt = wi < nwin ? *(const uint4 *)(row + 16 * wi) : uint4{0, 0, 0, 0};
+    for (; wi < nwin; wi += 64) {
+        const uint4 cur = nxt;
+        if (wi + 64 < nwin) nxt = *(const uint4 *)(row + 16 * (wi + 64));
+        const uint32_t d[4] = {cur.x, cur.y, cur.z, cur.w};
+        // The cursor inside this window: code q, sub-code sp, position ii.
+        uint32_t q = 0, sp = 0, ii = 0;
+        auto code_at = [&](uint32_t qq) -> uint32_t {
+            const uint32_t b = qq * (uint32_t)W.cb;
+            const uint32_t dw = b >> 2;
+            const uint32_t x = dw == 0 ? d[0] : dw == 1 ? d[1] : dw == 2 ? d[2] : d[3];
+            return W.cb == 1 ? (x >> (8 * (b & 3))) & 0xFFu : (x >> (8 * (b & 3))) & 0xFFFFu;
+        };
+        Walk w;
+        w.code = code_at(0);
+        w.sp = 0;
+        w.ii = 0;
+        walk_sub(W, w);
+        const uint64_t e0 = wi * E;
+        for (uint64_t g = 0; g < E; g += 16) {
+            int8_t av[MR][16];
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                if ((uint64_t)r < G.m) *(uint4 *)av[r] = *(const uint4 *)(G.a + (int64_t)r * G.ars + (int64_t)(e0 + g));
+                else *(uint4 *)av[r] = uint4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int wv = walk_value_t<TIER>(W, w);
+#pragma unroll
+                for (int r = 0; r < MR; ++r) acc[r] += (int)av[r][e] * wv;
+                // advance inside the window
+                if (++ii == ib) {
+                    ii = 0;
+                    if (++sp == P) {
+                        sp = 0;
+                        if (++q < cpw) w.code = code_at(q);
+                    }
+                    w.sp = sp;
+                    walk_sub(W, w);
+                }
+                w.ii = ii;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        int64_t v = acc[r];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == r && (uint64_t)r < G.m)
+            finish_any(G.c + ((int64_t)r * G.crs + (int64_t)j * G.ccs) * G.ob, v, G);
+    }
+}
+
+// One-byte codes of 4 or 8 elements (Ternary<4,u8>, Sign<8,u8>,
+// Packed<Grid<4>,4>, Book<_, 4|8, u8>, ...), m <= 4: the table variant.  Each
+// workgroup first decodes all 256 codes into an LDS table of D = MAX_BLOCK / 4
+// packed dwords per code (four i8 values each, through the same decode), so a
+// code costs one byte extract, D LDS reads and D x MR v_dot4_i32_i8.  A wave
+// takes 4 columns: the A bytes of a window are loaded once for all four, and
+// each column's next code window is loaded before this one is used.
+template <int MR, int D>
+__global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvArgs G) {
+    __shared__ uint32_t lut[256 * D];
+    for (int idx = threadIdx.x; idx < 256 * D; idx += 256) {
+        const uint32_t code = (uint32_t)idx / D, part = (uint32_t)idx % D;
+        uint32_t v = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v |= (uint32_t)(uint8_t)dec(W.cd, code, 4 * part + e) << (8 * e);
+        lut[idx] = v;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const uint64_t jb = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    if (jb >= G.n) return;  // whole waves, after the barrier
+    const uint64_t nwin = W.per_row / 16;  // one-byte codes: a row is per_row bytes
+    constexpr int E = 64 * D;              // elements per 16-byte window
+    int acc[4][MR];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[c][r] = 0;
+    uint4 nxt[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        nxt[c] = ((uint64_t)lane < nwin && jb + c < G.n)
+                     ? *(const uint4 *)(W.codes + (jb + c) * W.per_row + 16 * (uint64_t)lane)
+                     : uint4{0, 0, 0, 0};
+    for (uint64_t wi = (uint64_t)lane; wi < nwin; wi += 64) {
+        uint4 cur[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            cur[c] = nxt[c];
+            if (wi + 64 < nwin && jb + c < G.n)
+                nxt[c] = *(const uint4 *)(W.codes + (jb + c) * W.per_row + 16 * (wi + 64));
+        }
+        uint32_t a[MR][E / 4];
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+            for (int h = 0; h < E / 16; ++h) {
+                uint4 v = uint4{0, 0, 0, 0};
+                if ((uint64_t)r < G.m) v = *(const uint4 *)(G.a + (int64_t)r * G.ars + (int64_t)(wi * E + 16 * h));
+                a[r][4 * h] = v.x;
+                a[r][4 * h + 1] = v.y;
+                a[r][4 * h + 2] = v.z;
+                a[r][4 * h + 3] = v.w;
+            }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t d[4] = {cur[c].x, cur[c].y, cur[c].z, cur[c].w};
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const uint32_t code = (d[q >> 2] >> (8 * (q & 3))) & 0xFFu;
+#pragma unroll
+                for (int part = 0; part < D; ++part) {
+                    const int wv = (int)lut[code * D + part];
+#pragma unroll
+                    for (int r = 0; r < MR; ++r)
+                        acc[c][r] = __builtin_amdgcn_sdot4((int)a[r][q * D + part], wv, acc[c][r], false);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            int64_t v = acc[c][r];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == c * MR + r && (uint64_t)r < G.m && jb + c < G.n)
+                finish_any(G.c + ((int64_t)r * G.crs + (int64_t)(jb + c) * G.ccs) * G.ob, v, G);
+        }
+}
+
+template <int MR>
+static void launch_gemv_lut(const CodedArgs &W, const GemvArgs &G, hipStream_t s) {
+    const dim3 grid((unsigned)((G.n + 15) / 16));
+    if (W.cd.mb == 4) hipLaunchKernelGGL((coded_gemv_lut_kernel<MR, 1>), grid, dim3(256), 0, s, W, G);
+    else hipLaunchKernelGGL((coded_gemv_lut_kernel<MR, 2>), grid, dim3(256), 0, s, W, G);
+}
+
+template <int TIER, int MR>
+static void launch_gemv_mr(const CodedArgs &W, const GemvArgs &G, bool win, dim3 grid, hipStream_t s) {
+    if (win) hipLaunchKernelGGL((coded_gemv_win_kernel<TIER, MR>), grid, dim3(256), 0, s, W, G);
+    else hipLaunchKernelGGL((coded_gemv_kernel<TIER, MR>), grid, dim3(256), 0, s, W, G);
+}
+
+template <int TIER>
+static void launch_gemv_t(const CodedArgs &W, const GemvArgs &G, bool win, dim3 grid, hipStream_t s) {
+    if (G.m <= 1) launch_gemv_mr<TIER, 1>(W, G, win, grid, s);
+    else if (G.m <= 2) launch_gemv_mr<TIER, 2>(W, G, win, grid, s);
+    else if (G.m <= 4) launch_gemv_mr<TIER, 4>(W, G, win, grid, s);
+    else launch_gemv_mr<TIER, 8>(W, G, win, grid, s);
+}
+
+static void launch_gemv(const CodedArgs &W, const GemvArgs &G, bool win, hipStream_t s) {
+    const dim3 grid((unsigned)((G.n + 3) / 4));
+    switch (W.cd.tier) {
+    case UOR_TIER_IDENTITY: launch_gemv_t<UOR_TIER_IDENTITY>(W, G, win, grid, s); break;
+    case UOR_TIER_GRID: launch_gemv_t<UOR_TIER_GRID>(W, G, win, grid, s); break;
+    case UOR_TIER_BOOK: launch_gemv_t<UOR_TIER_BOOK>(W, G, win, grid, s); break;
+    case UOR_TIER_SIGN: launch_gemv_t<UOR_TIER_SIGN>(W, G, win, grid, s); break;
+    default: launch_gemv_t<UOR_TIER_TERNARY>(W, G, win, grid, s); break;
+    }
+}
+
 struct DirectArgs {
     const int8_t *a;
     int64_t ars, acs;
@@ -329,6 +623,37 @@ extern "C" int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, 
     const uint64_t m = A.rows;
     hipStream_t s = (hipStream_t)stream;
 
+    if (transposed && k > 0 && m <= 8 && k <= GEMV_MAX_K && (n + 3) / 4 <= 0x7FFFFFFFull) {
+        const bool a_vec = A.cs == 1 && A.rs > 0 && (A.rs % 16) == 0 && ((uintptr_t)A.base & 15) == 0;
+        GemvArgs G{(const int8_t *)A.base, A.rs, A.cs, a_vec ? 1 : 0, C.base, C.rs, C.cs, m, k, n,
+                   alpha, beta, encode, out_type};
+        // Whole 16-byte code windows per row, a window a multiple of 16
+        // elements, 16-byte aligned codes and A rows.
+        const uint64_t row_bytes = W.per_row * (uint64_t)W.cb;
+        const bool win = a_vec && row_bytes % 16 == 0 && ((uintptr_t)codes & 15) == 0 &&
+                         ((16 / (uint64_t)W.cb) * W.cd.mb) % 16 == 0;
+        // The table variant: one-byte codes of 4 or 8 elements, m <= 4.
+        const bool lut = win && W.cb == 1 && (W.cd.mb == 4 || W.cd.mb == 8) && m <= 4 &&
+                         (n + 15) / 16 <= 0x7FFFFFFFull;
+        if (route) {
+            route->kind = UOR_ROUTE_CODED_GEMV;
+            route->tile_m = (int)m;
+            route->tile_n = lut ? 4 : 1;
+            route->tile_k = win ? (int)((16 / W.cb) * W.cd.mb) : (int)(((k + 63) / 64 + 15) / 16 * 16);
+            route->split_k = 64;
+            route->launches = 1;
+            route->operand_modes = lut ? 3 : win ? 2 : (a_vec ? 1 : 0);
+        }
+        if (lut) {
+            if (m <= 1) launch_gemv_lut<1>(W, G, s);
+            else if (m <= 2) launch_gemv_lut<2>(W, G, s);
+            else launch_gemv_lut<4>(W, G, s);
+        } else {
+            launch_gemv(W, G, win, s);
+        }
+        UOR_HIP(hipGetLastError());
+        return UOR_OK;
+    }
     const uint64_t wbytes = k ? decoded_bytes(k, n) : 0;
     const bool dense = k > 0 && scratch && scratch_bytes >= wbytes + uor_gfx950_suggested_scratch_i8(m, k, n) &&
                        (n + 127) / 128 <= 0x7FFFFFFFull && (k + 127) / 128 <= 65535ull &&
