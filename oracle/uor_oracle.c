@@ -286,6 +286,13 @@ int ora_gemm_int(int elem_bytes,
             i128 acc = 0;
             for (uint64_t p = 0; p < k; p++)
                 acc += load_int(a, at(&A, i, p), elem_bytes) * load_int(b, at(&B, p, j), elem_bytes);
+            /* gemm_packed_impl's modular route (kernel.rs:566-607): Wrapping
+             * into an output of at most 32 bits adds in Z/2^32 and hands
+             * Linear::finish the lane sign-extended (modular_spec and
+             * modular_as_acc for i8/i16/i32, kernel.rs:185-221, 250-279,
+             * 308-330).  Only the scaling can tell the two apart: alpha * X
+             * saturates at 2^127 where alpha * (X mod 2^32) does not. */
+            if (mode == 3 && out_bytes <= 4) acc = (i128)(int32_t)(uint32_t)(u128)acc;
             int reads = beta != 0;
             i128 prior = reads ? load_int(c, ci, out_bytes) : 0;
             store_int(c, ci, out_bytes, linear_finish_i128(acc, reads, prior, alpha, beta, out_bytes, mode));

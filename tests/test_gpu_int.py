@@ -159,3 +159,27 @@ def test_numpy_cx10_fixtures(uor, dev):
             torch.cuda.synchronize()
             assert st == 0
             assert np.array_equal(c.cpu().numpy(), blobs["expected"]), (case["stem"], route)
+
+
+@pytest.mark.parametrize("offer", [True, False])
+def test_wrapping_narrow_output_is_the_modular_lane(oracle, uor, dev, offer):
+    """Wrapping into at most 32 bits scales the sum in Z/2^32 (the public
+    route's modular lane), so alpha = 2^63 - 1 on i32 elements near their
+    extremes wraps instead of saturating; wider outputs saturate first.  The
+    closed form (all 2^31 - 1, k = 8): -8 for i32/i16 outputs, -1 for i64."""
+    k = 8
+    a = np.full(k, (1 << 31) - 1, np.int32)
+    for out, want in (("i32", -8), ("i16", -8), ("i64", -1)):
+        run(oracle, uor, dev, 4, 1, k, 1, out=out, alpha=(1 << 63) - 1, encode="wrapping",
+            offer=offer, a=a, b=a.copy())
+        c = torch.zeros(1, dtype={"i32": torch.int32, "i16": torch.int16, "i64": torch.int64}[out],
+                        device=dev)
+        st, _ = uor.gemm_int(torch.from_numpy(a).to(dev), (1, k), (k, 1),
+                             torch.from_numpy(a).to(dev), (k, 1), (1, 1), c, (1, 1), (1, 1),
+                             out=out, alpha=(1 << 63) - 1, encode="wrapping")
+        torch.cuda.synchronize()
+        assert st == 0 and int(c.cpu()[0]) == want, out
+    # full-range operands, large scalars, every narrow output
+    for out in ("i8", "i16", "i32"):
+        run(oracle, uor, dev, 4, 17, 300, 23, out=out, alpha=(1 << 63) - 1, beta=-(1 << 62),
+            encode="wrapping", offer=offer, seed=31)

@@ -171,3 +171,29 @@ def test_errors(oracle):
     assert oracle.gemm_int(a, (3, 4), (4, 1), a, (3, 4), (4, 1), c, (3, 4), (4, 1)) == "nonconformant"
     assert oracle.gemm_int(a, (3, 4), (4, 1), a, (4, 3), (3, 1), c, (3, 3), (1, 1)) == "output_aliases_itself"
     assert oracle.gemm_int(a, (3, 5), (5, 1), a, (5, 3), (3, 1), c, (3, 3), (3, 1)) == "short_buffer"
+
+
+def test_wrapping_narrow_output_is_the_modular_lane(oracle):
+    """gemm_packed_impl (kernel.rs:566-607): Wrapping into at most 32 bits
+    runs the Z/2^32 lane and scales the lane's value, so alpha * X never
+    saturates; wider outputs, or other encodes, scale the exact X with
+    saturating_mul.  Closed form: i32 elements all 2^31 - 1, k = 8, so
+    X = 8 (2^31 - 1)^2 = 2^65 - 2^35 + 8 and X mod 2^32 = 8; alpha = 2^63 - 1:
+      Wrapping -> i32, i16: 8 (2^63 - 1) = 2^66 - 8, which wraps to -8
+      Wrapping -> i64: alpha * X >= 2^127 saturates to i128::MAX, wraps to -1
+      Nearest  -> i32: saturates to i32::MAX.
+    (Scaling the exact X would give -1 for the narrow outputs too.)"""
+    k = 8
+    a = np.full(k, (1 << 31) - 1, np.int32)
+    cases = [("wrapping", np.int32, -8), ("wrapping", np.int64, -1),
+             ("nearest", np.int32, (1 << 31) - 1), ("wrapping", np.int16, -8)]
+    for mode, dt, want in cases:
+        c = np.zeros(1, dt)
+        assert oracle.gemm_int(a, (1, k), (k, 1), a, (k, 1), (1, 1), c, (1, 1), (1, 1),
+                               alpha=(1 << 63) - 1, encode=mode) == "ok"
+        assert int(c[0]) == want, (mode, dt)
+    # beta scales C in the same way on both routes: C = 3, beta = 2^62.
+    c = np.array([3], np.int32)
+    assert oracle.gemm_int(a, (1, k), (k, 1), a, (k, 1), (1, 1), c, (1, 1), (1, 1),
+                           alpha=1, beta=1 << 62, encode="wrapping") == "ok"
+    assert int(c[0]) == 8  # 8 + 3 * 2^62 mod 2^32

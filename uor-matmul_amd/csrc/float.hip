@@ -1477,7 +1477,14 @@ __device__ inline W192 int_direct_sum(const IArgs &F, uint64_t i, uint64_t j) {
 // i128, impl_encode_from_limbs acc.rs:405-442 for Limbs<3>).
 template <int OB>
 __device__ inline void int_finish(const IArgs &F, char *cp, const W192 &x) {
-    const i128 low = (i128)(((u128)x.w[1] << 64) | x.w[0]);
+    i128 low = (i128)(((u128)x.w[1] << 64) | x.w[0]);
+    // The public route's modular lane (kernel.rs:566-607, modular_spec and
+    // modular_as_acc at :185-221, 250-279, 308-330): Wrapping into at most
+    // 32 bits hands Linear::finish the sum in Z/2^32, sign-extended, so alpha
+    // scales that lane and never saturates.  (i64 elements: Z/2^64 for
+    // outputs of at most 64 bits, which with alpha = 1, beta = 0 wraps to the
+    // same bytes as the exact value.)
+    if (!F.limbs && OB <= 4 && F.mode == UOR_ENCODE_WRAPPING) low = (i128)(int32_t)(uint32_t)x.w[0];
     if (!F.limbs) {
         // i16 / i32 elements: |X| < 2^126, the i128 accumulator.
         if (F.alpha == 1 && F.beta == 0) {
