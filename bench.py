@@ -564,18 +564,24 @@ def bench_int(args, torch, uor):
         st, _ = uor.gemm_int(a, (R, N), (N, 1), b, (N, N), (N, 1), slab, (R, N), (N, 1), out=outt)
         torch.cuda.synchronize()
         parity = st == 0 and bool(torch.equal(slab, c[:R * N * rec]))
-        off = (-sc.data_ptr()) % 256
-        plan = sc[off:off + 12].cpu().view(torch.int32).tolist()
-        nmod = plan[0]
-        kp = (N + 63) // 64 * 64
-        issued = 2.0 * N * N * kp * nmod / (ms * 1e-3) / 1e12
-        out.append({"elements": f"i{8 * eb}", "m": N, "n": N, "k": N, "out": outt,
-                    "route": route.get("kind"), "ms_per_call": round(ms, 4),
-                    "exact_TOPS": round(2.0 * N ** 3 / (ms * 1e-3) / 1e12, 2),
-                    "moduli": nmod, "bound_bits": plan[2],
-                    "int8_TOPS_issued": round(issued, 1),
-                    "frac_int8_mfma_peak": round(issued / PEAK_INT8_TOPS, 4),
-                    "parity_vs_direct_route_64_rows": parity})
+        rec_ = {"elements": f"i{8 * eb}", "m": N, "n": N, "k": N, "out": outt,
+                "route": route.get("kind"), "ms_per_call": round(ms, 4),
+                "exact_TOPS": round(2.0 * N ** 3 / (ms * 1e-3) / 1e12, 2)}
+        if route.get("kind") == "int_limb":
+            # L = eb limbs per element: L^2 int8 products per exact product.
+            issued = 2.0 * N ** 3 * eb * eb / (ms * 1e-3) / 1e12
+            rec_.update({"limbs": eb, "plane_gemms": route.get("split_k")})
+        else:
+            off = (-sc.data_ptr()) % 256
+            plan = sc[off:off + 12].cpu().view(torch.int32).tolist()
+            nmod = plan[0]
+            kp = (N + 63) // 64 * 64
+            issued = 2.0 * N * N * kp * nmod / (ms * 1e-3) / 1e12
+            rec_.update({"moduli": nmod, "bound_bits": plan[2]})
+        rec_.update({"int8_TOPS_issued": round(issued, 1),
+                     "frac_int8_mfma_peak": round(issued / PEAK_INT8_TOPS, 4),
+                     "parity_vs_direct_route_64_rows": parity})
+        out.append(rec_)
         del a, b, c, sc, slab
         torch.cuda.empty_cache()
     return out

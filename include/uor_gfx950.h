@@ -96,6 +96,7 @@ typedef struct uor_view {
 #define UOR_ROUTE_TROP_SELECTED_DIRECT 32 /* max-plus + witness, per-cell loop (k > 2^21) */
 #define UOR_ROUTE_INT_CRT 40      /* i16/i32/i64 elements: int8 residue MFMA + CRT */
 #define UOR_ROUTE_INT_DIRECT 41   /* i16/i32/i64 elements: per-cell exact loop */
+#define UOR_ROUTE_INT_LIMB 42     /* i16/i32 elements: int8 limb planes on the dense int8 route */
 typedef struct uor_route {
     int32_t kind;
     int32_t tile_m, tile_n, tile_k;

@@ -72,7 +72,8 @@ def test_shapes_against_oracle(oracle, uor, dev, eb, m, k, n, offer):
     alpha, beta = (1, 0) if eb == 8 else (3, -1)
     route = run(oracle, uor, dev, eb, m, k, n, alpha=alpha, beta=beta, offer=offer,
                 seed=eb * 1000 + m + k + n)
-    assert route["kind"] == ("int_crt" if offer else "int_direct"), route
+    want = ("int_limb" if eb < 8 else "int_crt") if offer else "int_direct"
+    assert route["kind"] == want, route
 
 
 @pytest.mark.parametrize("out", ["i8", "i16", "i32", "i64", "i128"])
@@ -115,6 +116,39 @@ def test_depth_chunks(oracle, uor, dev, eb):
     mod p: k = 2^17 + 192 is two chunks (the second short)."""
     route = run(oracle, uor, dev, eb, 16, (1 << 17) + 192, 24, alpha=3, beta=-1, seed=11)
     assert route["kind"] == "int_crt" and route["split_k"] == 2, route
+
+
+def test_residue_route_past_the_limb_depth(oracle, uor, dev):
+    """i32 elements at L k >= 2^17 (k = 2^15 + 40) under Nearest: the limb
+    planes would not be exact in i32, so the residue route runs."""
+    route = run(oracle, uor, dev, 4, 9, (1 << 15) + 40, 11, alpha=3, beta=-1, seed=12)
+    assert route["kind"] == "int_crt" and route["split_k"] == 1, route
+
+
+@pytest.mark.parametrize("out", ["i8", "i16", "i32"])
+def test_limb_route_modular_depth(oracle, uor, dev, out):
+    """Wrapping into at most 32 bits: the limb planes are only needed mod
+    2^32, so the limb route takes any depth and drops the shifts past 32 bits
+    (i32 elements: 4 of 7 plane GEMMs)."""
+    route = run(oracle, uor, dev, 4, 9, (1 << 15) + 40, 11, out=out, alpha=(1 << 63) - 1,
+                beta=-(1 << 62), encode="wrapping", seed=13)
+    assert route["kind"] == "int_limb" and route["split_k"] == 4, route
+    route = run(oracle, uor, dev, 2, 9, (1 << 16) + 40, 11, out=out, alpha=5, beta=3,
+                encode="wrapping", seed=14)
+    assert route["kind"] == "int_limb" and route["split_k"] == 3, route
+
+
+@pytest.mark.parametrize("eb", [2, 4])
+def test_limb_route_extremes(oracle, uor, dev, eb):
+    """Every element at MIN (or MAX) at the deepest exact limb depth (L k just
+    below 2^17): each plane GEMM sums L k products of magnitude 2^14."""
+    info = np.iinfo(DT[eb])
+    k = (1 << 17) // eb - 1
+    for v in (info.min, info.max):
+        a = np.full(3 * k, v, DT[eb])
+        b = np.full(k * 2, info.min, DT[eb])
+        route = run(oracle, uor, dev, eb, 3, k, 2, out="i128", a=a, b=b, seed=15)
+        assert route["kind"] == "int_limb" and route["split_k"] == 2 * eb - 1, route
 
 
 def test_k_zero_and_empty(oracle, uor, dev):

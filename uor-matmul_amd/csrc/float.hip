@@ -1789,13 +1789,196 @@ extern "C" int uor_gfx950_dgemm(uint64_t m, uint64_t k, uint64_t n, int64_t alph
                     scratch_bytes, stream);
 }
 
+// ------------------------------------------------------------ limb route --
+//
+// i16 / i32 elements as L = EB int8 limbs on the dense int8 route.  With
+// l_t = ((a >> 8t) & 0xFF) - 128 for t < L - 1, l_{L-1} = a >> 8(L-1) and
+// Ca = 128 (1 + 256 + ... + 256^{L-2}):  a = sum_t 256^t l_t + Ca, so
+//   sum_p a b = sum_s 256^s G_s + Ca (RA_i + RB_j) - Ca^2 k,
+// G_s = sum over t + u = s of the int8 products of limb planes t and u,
+// RA_i = sum_p a[i,p], RB_j = sum_p b[p,j].  A's limbs sit side
+// by side (m x Lk, plane t at column tk) and B's in reverse order (Lk x n,
+// plane u at row (L-1-u)k), so each G_s is one GEMM over a contiguous window
+// of both: depth (pairs of s) x k.  The planes hold G_s in i32: exact when
+// Lk < 2^17 (|G_s| <= 2^14 L k), and for Wrapping into at most 32 bits --
+// where only the sum mod 2^32 is used -- for any depth, with the shifts past
+// 32 bits left out.
+constexpr int LIMB_SPLIT_A = 16;   // A elements per thread
+constexpr int LIMB_SPLIT_B = 64;   // B rows per thread
+
+template <int EB>
+__device__ inline int8_t limb_of(int64_t v, int t) {
+    constexpr int L = EB;
+    if (t == L - 1) return (int8_t)(v >> (8 * (L - 1)));
+    return (int8_t)((int)((v >> (8 * t)) & 0xFF) - 128);
+}
+
+__global__ void __launch_bounds__(256) fill_i64_kernel(int64_t *p, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+// Thread: LIMB_SPLIT_A consecutive p of row blockIdx.y; a block's partial
+// row sum is added once.
+template <int EB>
+__global__ void __launch_bounds__(256) limb_split_a_kernel(IArgs F, int8_t *acat, int64_t *sa) {
+    constexpr int L = EB;
+    __shared__ int64_t part[4];
+    const uint64_t i = blockIdx.y;
+    const uint64_t p0 = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * LIMB_SPLIT_A;
+    int64_t sum = 0;
+    if (p0 < F.k) {
+        int8_t l[L][LIMB_SPLIT_A];
+#pragma unroll
+        for (int e = 0; e < LIMB_SPLIT_A; ++e) {
+            const int64_t v = p0 + e < F.k ? load_ielem<EB>(F.a, (int64_t)i * F.ars + (int64_t)(p0 + e) * F.acs) : 0;
+            sum += v;
+#pragma unroll
+            for (int t = 0; t < L; ++t) l[t][e] = limb_of<EB>(v, t);
+        }
+        int8_t *row = acat + i * (L * F.k);
+#pragma unroll
+        for (int t = 0; t < L; ++t)
+#pragma unroll
+            for (int e = 0; e < LIMB_SPLIT_A; ++e)
+                if (p0 + e < F.k) row[(uint64_t)t * F.k + p0 + e] = l[t][e];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd((unsigned long long *)&sa[i], (unsigned long long)(part[0] + part[1] + part[2] + part[3]));
+}
+
+// Thread: column j, LIMB_SPLIT_B consecutive rows of B.
+template <int EB>
+__global__ void __launch_bounds__(256) limb_split_b_kernel(IArgs F, int8_t *brev, int64_t *sb) {
+    constexpr int L = EB;
+    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t p0 = (uint64_t)blockIdx.y * LIMB_SPLIT_B;
+    if (j >= F.n) return;
+    int64_t sum = 0;
+    for (int e = 0; e < LIMB_SPLIT_B && p0 + e < F.k; ++e) {
+        const uint64_t p = p0 + e;
+        const int64_t v = load_ielem<EB>(F.b, (int64_t)p * F.brs + (int64_t)j * F.bcs);
+        sum += v;
+#pragma unroll
+        for (int t = 0; t < L; ++t) brev[((uint64_t)(L - 1 - t) * F.k + p) * F.n + j] = limb_of<EB>(v, t);
+    }
+    atomicAdd((unsigned long long *)&sb[j], (unsigned long long)sum);
+}
+
+// One thread per cell: X from the planes and the line sums (two's-complement
+// i128 arithmetic, exact when the planes are, right mod 2^32 otherwise), then
+// Linear::finish and the encode.
+__global__ void __launch_bounds__(256) limb_combine_kernel(IArgs F, const int32_t *planes, int nplanes,
+                                                           const int64_t *sa, const int64_t *sb, int64_t ca) {
+    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
+    if (j >= F.n) return;
+    const uint64_t cell = i * F.n + j, mn = F.m * F.n;
+    u128 x = 0;
+    for (int sft = nplanes - 1; sft >= 0; --sft) x = (x << 8) + (u128)(i128)planes[(uint64_t)sft * mn + cell];
+    x += (u128)((i128)ca * ((i128)sa[i] + (i128)sb[j]));
+    x -= (u128)((i128)ca * (i128)ca * (i128)F.k);
+    const i128 v = (i128)x;
+    W192 w{{(uint64_t)x, (uint64_t)(x >> 64), v < 0 ? ~(uint64_t)0 : 0}};
+    char *cp = F.c + ((int64_t)i * F.crs + (int64_t)j * F.ccs) * F.ob;
+    switch (F.ob) {
+    case 1: int_finish<1>(F, cp, w); break;
+    case 2: int_finish<2>(F, cp, w); break;
+    case 4: int_finish<4>(F, cp, w); break;
+    case 8: int_finish<8>(F, cp, w); break;
+    default: int_finish<16>(F, cp, w); break;
+    }
+}
+
+struct LimbLayout {
+    uint64_t acat, brev, planes, sa, sb, rest;  // byte offsets
+    int nplanes;
+    bool modular;
+};
+
+static uint64_t up256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
+
+// The limb route's plan, or nplanes = 0 when it does not apply.
+static LimbLayout limb_layout(int eb, uint64_t m, uint64_t k, uint64_t n, int out_type, int encode) {
+    LimbLayout Y{};
+    if (!(eb == 2 || eb == 4) || m == 0 || n == 0 || k == 0) return Y;
+    const uint64_t L = (uint64_t)eb;
+    Y.modular = encode == UOR_ENCODE_WRAPPING && out_type <= 4;
+    if (!Y.modular && L * k >= (1ull << 17)) return Y;
+    if (m > 65535 || (n + 255) / 256 > 0x7fffffffull || (k + 255 * LIMB_SPLIT_A) / (256 * LIMB_SPLIT_A) > 0x7fffffffull ||
+        (k + LIMB_SPLIT_B - 1) / LIMB_SPLIT_B > 65535)
+        return Y;
+    Y.nplanes = (int)(2 * L - 1);
+    if (Y.modular && Y.nplanes > 4) Y.nplanes = 4;  // 256^s G_s vanishes mod 2^32 for s >= 4
+    Y.acat = 0;
+    Y.brev = up256(m * L * k);
+    Y.planes = Y.brev + up256(L * k * n);
+    Y.sa = Y.planes + up256((uint64_t)Y.nplanes * m * n * 4);
+    Y.sb = Y.sa + up256(m * 8);
+    Y.rest = Y.sb + up256(n * 8);
+    return Y;
+}
+
+// The limb route's scratch: its buffers plus the dense route's own offer at
+// the deepest plane GEMM.
+static uint64_t limb_scratch(int eb, uint64_t m, uint64_t k, uint64_t n, int out_type, int encode) {
+    const LimbLayout Y = limb_layout(eb, m, k, n, out_type, encode);
+    if (!Y.nplanes) return 0;
+    return Y.rest + uor_gfx950_suggested_scratch_i8(m, (uint64_t)eb * k, n) + 256;
+}
+
+template <int EB>
+static int launch_int_limb(const IArgs &F, char *sc, uint64_t have, const LimbLayout &Y, hipStream_t s,
+                           int *launches) {
+    constexpr int L = EB;
+    const uint64_t m = F.m, k = F.k, n = F.n;
+    int8_t *acat = (int8_t *)(sc + Y.acat), *brev = (int8_t *)(sc + Y.brev);
+    int32_t *planes = (int32_t *)(sc + Y.planes);
+    int64_t *sa = (int64_t *)(sc + Y.sa), *sb = (int64_t *)(sc + Y.sb);
+    hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, sa, m);
+    hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sb, n);
+    hipLaunchKernelGGL(limb_split_a_kernel<EB>,
+                       dim3((unsigned)((k + 256 * LIMB_SPLIT_A - 1) / (256 * LIMB_SPLIT_A)), (unsigned)m), dim3(256),
+                       0, s, F, acat, sa);
+    hipLaunchKernelGGL(limb_split_b_kernel<EB>,
+                       dim3((unsigned)((n + 255) / 256), (unsigned)((k + LIMB_SPLIT_B - 1) / LIMB_SPLIT_B)), dim3(256),
+                       0, s, F, brev, sb);
+    UOR_HIP(hipGetLastError());
+    *launches = 4;
+    for (int sft = 0; sft < Y.nplanes; ++sft) {
+        const int t0 = sft - (L - 1) > 0 ? sft - (L - 1) : 0, t1 = sft < L - 1 ? sft : L - 1;
+        const uint64_t depth = (uint64_t)(t1 - t0 + 1) * k;
+        const uint64_t v0 = (uint64_t)(L - 1 - sft + t0);
+        const uor_view av{acat + (uint64_t)t0 * k, m * (uint64_t)L * k - (uint64_t)t0 * k, m, depth,
+                          (int64_t)((uint64_t)L * k), 1};
+        const uor_view bv{brev + v0 * k * n, (uint64_t)L * k * n - v0 * k * n, depth, n, (int64_t)n, 1};
+        const uor_view cv{planes + (uint64_t)sft * m * n, m * n, m, n, (int64_t)n, 1};
+        uor_route r{};
+        const int st = uor_gfx950_gemm_i8(&av, &bv, &cv, UOR_OUT_I32, 1, 0,
+                                          Y.modular ? UOR_ENCODE_WRAPPING : UOR_ENCODE_NEAREST, sc + Y.rest,
+                                          have - Y.rest, (void *)s, &r);
+        if (st) return st;
+        *launches += r.launches;
+    }
+    const int64_t ca = L == 2 ? 128 : 128 * (1 + 256 + 65536);
+    hipLaunchKernelGGL(limb_combine_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)m), dim3(256), 0, s, F,
+                       planes, Y.nplanes, sa, sb, ca);
+    UOR_HIP(hipGetLastError());
+    *launches += 1;
+    return UOR_OK;
+}
+
 extern "C" uint64_t uor_gfx950_suggested_scratch_int(int elem_bytes, uint64_t m, uint64_t k,
                                                      uint64_t n) {
     if (elem_bytes == 1) return uor_gfx950_suggested_scratch_i8(m, k, n);
     if (!(elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8)) return 0;
     if (m == 0 || n == 0 || k == 0) return 0;
     const uint64_t kc = std::min<uint64_t>(k, CRT_BK_MAX);
-    return crt_layout(m, kc, n, int_moduli_cap(elem_bytes, k), 1).total + 256;
+    const uint64_t crt = crt_layout(m, kc, n, int_moduli_cap(elem_bytes, k), 1).total + 256;
+    // Enough for the limb route under any encode and output (exact planes).
+    return std::max(crt, limb_scratch(elem_bytes, m, k, n, UOR_OUT_I64, UOR_ENCODE_NEAREST));
 }
 
 extern "C" int uor_gfx950_gemm_int(int elem_bytes, const uor_view *a, const uor_view *b,
@@ -1825,6 +2008,29 @@ extern "C" int uor_gfx950_gemm_int(int elem_bytes, const uor_view *a, const uor_
     // The residue route when the offer holds planes: as many moduli as the
     // element width can need at this depth, or as many as fit (the device
     // plan sends every cell to the per-cell loop if the data needs more).
+    // The limb route first: i16 / i32 elements at depths whose limb planes
+    // are exact in i32 (any depth for Wrapping into at most 32 bits).
+    if (scratch && F.k > 0) {
+        const LimbLayout Y = limb_layout(elem_bytes, F.m, F.k, F.n, out_type, encode);
+        const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+        const uint64_t have = scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
+        if (Y.nplanes && have >= Y.rest + uor_gfx950_suggested_scratch_i8(F.m, (uint64_t)elem_bytes * F.k, F.n)) {
+            int launches = 0;
+            const int st2 = elem_bytes == 2 ? launch_int_limb<2>(F, (char *)p1, have, Y, s, &launches)
+                                            : launch_int_limb<4>(F, (char *)p1, have, Y, s, &launches);
+            if (st2) return st2;
+            if (route) {
+                route->kind = UOR_ROUTE_INT_LIMB;
+                route->tile_m = route->tile_n = 256;
+                route->tile_k = DL_BK;
+                route->split_k = Y.nplanes;  // plane GEMMs
+                route->launches = launches;
+                route->moduli = elem_bytes;  // limbs per element
+                route->scratch_used = Y.rest;
+            }
+            return UOR_OK;
+        }
+    }
     int nm = 0;
     CrtLayout L{};
     char *sc = nullptr;

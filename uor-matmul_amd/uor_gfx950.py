@@ -24,7 +24,7 @@ STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buf
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
           10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill",
           13: "coded_dense", 14: "coded_direct", 15: "coded_gemv", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
-          31: "trop_selected", 32: "trop_selected_direct", 40: "int_crt", 41: "int_direct"}
+          31: "trop_selected", 32: "trop_selected_direct", 40: "int_crt", 41: "int_direct", 42: "int_limb"}
 WITNESS = {"lexicographic": 0, "compare_pass": 1}
 
 # Every symbol include/uor_gfx950.h declares.
