@@ -174,6 +174,18 @@ def test_larger_shapes_dense_route(oracle, uor, dev, name, transposed):
     assert st == "ok" and route["kind"] == "coded_dense", route
 
 
+@pytest.mark.parametrize("name", ["ternary4_u8", "sign8_u8", "packed_sign2_p4", "packed_grid4_p4",
+                                  "packed_book4x2_p2", "offset_ternary_wraps"])
+def test_dense_route_code_table_decode(oracle, uor, dev, name):
+    """W n x k with one-byte codes of 4 or 8 elements in whole 16-byte row
+    runs (k a multiple of 128): the decode into the scratch expands codes
+    through a per-workgroup table; n ragged against the 128-column tile."""
+    for k in (128, 640):
+        st, route = run(oracle, uor, dev, SPECS[name], 40, k, 200, True, True, alpha=-3, beta=2,
+                        seed=k + len(name))
+        assert st == "ok" and route["kind"] == "coded_dense", route
+
+
 @pytest.mark.parametrize("out", ["i8", "i16", "i32", "i64"])
 @pytest.mark.parametrize("encode", ["nearest", "wrapping"])
 @pytest.mark.parametrize("offer", [True, False])

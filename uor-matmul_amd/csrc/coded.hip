@@ -179,6 +179,60 @@ __global__ void __launch_bounds__(256) coded_decode_t_kernel(CodedArgs W, uint64
     }
 }
 
+// The same tile for one-byte codes of 4 or 8 elements whose rows are whole
+// 16-byte runs: the workgroup first decodes all 256 codes into an LDS table
+// of D = MAX_BLOCK / 4 packed dwords, then each thread loads its 64 elements'
+// codes with one 16-byte (D = 1) or 8-byte (D = 2) load and expands them
+// through the table.
+template <int D>
+__global__ void __launch_bounds__(256) coded_decode_t_lut_kernel(CodedArgs W, uint64_t k, uint64_t n, int8_t *out,
+                                                                 uint64_t ldw) {
+    __shared__ __attribute__((aligned(16))) int8_t tile[128][128];
+    __shared__ uint32_t lut[256 * D];
+    const int t = threadIdx.x;
+    for (int idx = t; idx < 256 * D; idx += 256) {
+        const uint32_t code = (uint32_t)idx / D, part = (uint32_t)idx % D;
+        uint32_t v = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v |= (uint32_t)(uint8_t)dec(W.cd, code, 4 * part + e) << (8 * e);
+        lut[idx] = v;
+    }
+    __syncthreads();
+    const uint64_t j0 = (uint64_t)blockIdx.x * 128, k0 = (uint64_t)blockIdx.y * 128;
+    const int cl = t & 127, kh = t >> 7;
+    const uint64_t j = j0 + cl, p0 = k0 + 64 * kh;
+    constexpr int NC = 16 / D;  // codes of this thread's 64 elements
+    if (j < n && p0 < k) {
+        const uint8_t *src = W.codes + j * W.per_row + p0 / (4 * D);
+        uint32_t cw[4];
+        if constexpr (D == 1) {
+            const uint4 x = *(const uint4 *)src;
+            cw[0] = x.x, cw[1] = x.y, cw[2] = x.z, cw[3] = x.w;
+        } else {
+            const uint2 x = *(const uint2 *)src;
+            cw[0] = x.x, cw[1] = x.y, cw[2] = 0, cw[3] = 0;
+        }
+#pragma unroll
+        for (int q = 0; q < NC; ++q) {
+            const uint32_t code = (cw[q >> 2] >> (8 * (q & 3))) & 0xFFu;
+#pragma unroll
+            for (int part = 0; part < D; ++part) {
+                const uint32_t v = lut[code * D + part];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tile[64 * kh + q * 4 * D + 4 * part + e][cl] = (int8_t)(v >> (8 * e));
+            }
+        }
+    }
+    __syncthreads();
+    const int ch = t & 7;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int r = pass * 32 + (t >> 3);
+        const uint64_t kk = k0 + r, jc = j0 + 16 * ch;
+        if (kk < k && jc < ldw) *(uint4 *)(out + kk * ldw + jc) = *(const uint4 *)&tile[r][16 * ch];
+    }
+}
+
 // W k x n (coded_gemm): the rows are already the output's; each thread walks
 // 16 consecutive elements of one row and stores them as one 16-byte chunk
 // (zeros past column n, inside the row stride).
@@ -663,7 +717,16 @@ extern "C" int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, 
         int8_t *wt = (int8_t *)scratch;
         if (transposed) {
             const dim3 grid((unsigned)((n + 127) / 128), (unsigned)((k + 127) / 128));
-            hipLaunchKernelGGL(coded_decode_t_kernel, grid, dim3(256), 0, s, W, k, n, wt, ldw);
+            // One-byte codes of 4 or 8 elements in whole 16-byte row runs,
+            // 16-byte aligned: the table variant.
+            const bool lut = W.cb == 1 && (W.cd.mb == 4 || W.cd.mb == 8) && W.per_row % 16 == 0 &&
+                             ((uintptr_t)codes & 15) == 0;
+            if (lut && W.cd.mb == 4)
+                hipLaunchKernelGGL(coded_decode_t_lut_kernel<1>, grid, dim3(256), 0, s, W, k, n, wt, ldw);
+            else if (lut)
+                hipLaunchKernelGGL(coded_decode_t_lut_kernel<2>, grid, dim3(256), 0, s, W, k, n, wt, ldw);
+            else
+                hipLaunchKernelGGL(coded_decode_t_kernel, grid, dim3(256), 0, s, W, k, n, wt, ldw);
         } else {
             const uint64_t blocks = (k * (ldw / 16) + 255) / 256;
             hipLaunchKernelGGL(coded_decode_kernel, dim3((unsigned)blocks), dim3(256), 0, s, W, k, n, wt, ldw);

@@ -1829,19 +1829,50 @@ __global__ void __launch_bounds__(256) limb_split_a_kernel(IArgs F, int8_t *acat
     int64_t sum = 0;
     if (p0 < F.k) {
         int8_t l[L][LIMB_SPLIT_A];
+        int64_t v[LIMB_SPLIT_A];
+        const char *src = F.a + ((int64_t)i * F.ars + (int64_t)p0 * F.acs) * EB;
+        if (F.acs == 1 && p0 + LIMB_SPLIT_A <= F.k && ((uintptr_t)src & 15) == 0) {
+            // EB 16-byte loads of the chunk's LIMB_SPLIT_A elements
 #pragma unroll
-        for (int e = 0; e < LIMB_SPLIT_A; ++e) {
-            const int64_t v = p0 + e < F.k ? load_ielem<EB>(F.a, (int64_t)i * F.ars + (int64_t)(p0 + e) * F.acs) : 0;
-            sum += v;
+            for (int q = 0; q < EB; ++q) {
+                const uint4 x = ((const uint4 *)src)[q];
+                const uint32_t d[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-            for (int t = 0; t < L; ++t) l[t][e] = limb_of<EB>(v, t);
-        }
-        int8_t *row = acat + i * (L * F.k);
-#pragma unroll
-        for (int t = 0; t < L; ++t)
+                for (int h = 0; h < 16 / EB; ++h) {
+                    const uint32_t dw = d[(h * EB) / 4];
+                    if constexpr (EB == 2) v[q * 8 + h] = (int16_t)(dw >> (16 * (h & 1)));
+                    else v[q * 4 + h] = (int32_t)dw;
+                }
+            }
+        } else {
 #pragma unroll
             for (int e = 0; e < LIMB_SPLIT_A; ++e)
-                if (p0 + e < F.k) row[(uint64_t)t * F.k + p0 + e] = l[t][e];
+                v[e] = p0 + e < F.k ? load_ielem<EB>(F.a, (int64_t)i * F.ars + (int64_t)(p0 + e) * F.acs) : 0;
+        }
+#pragma unroll
+        for (int e = 0; e < LIMB_SPLIT_A; ++e) {
+            sum += v[e];
+#pragma unroll
+            for (int t = 0; t < L; ++t) l[t][e] = limb_of<EB>(v[e], t);
+        }
+        int8_t *row = acat + i * (L * F.k);
+        // 16-byte stores when the chunk is whole and k keeps planes aligned.
+        const bool vec = p0 + LIMB_SPLIT_A <= F.k && (F.k % 16) == 0;
+#pragma unroll
+        for (int t = 0; t < L; ++t) {
+            if (vec) {
+                uint32_t w[4];
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    w[d] = (uint32_t)(uint8_t)l[t][4 * d] | ((uint32_t)(uint8_t)l[t][4 * d + 1] << 8) |
+                           ((uint32_t)(uint8_t)l[t][4 * d + 2] << 16) | ((uint32_t)(uint8_t)l[t][4 * d + 3] << 24);
+                *(uint4 *)(row + (uint64_t)t * F.k + p0) = uint4{w[0], w[1], w[2], w[3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < LIMB_SPLIT_A; ++e)
+                    if (p0 + e < F.k) row[(uint64_t)t * F.k + p0 + e] = l[t][e];
+            }
+        }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
