@@ -59,3 +59,37 @@ def test_validation_statuses_without_a_gpu():
     assert call(_v(P, 100, 5, 1, 1 << 62, 1), _v(P, 1, 1, 1, 1, 1), _v(P, 5, 5, 1, 1, 1)) == 3
     # The slice face: a short slice is status 3 (does_not_fit, slice.rs:104-116).
     assert lib.uor_gfx950_slice_gemm_i8(4, 4, 4, P, 15, P, 16, P, 16, 4, None, 0, None) == 3
+
+
+def test_coded_and_witness_validation_without_a_gpu():
+    """gemm_coded and gemm_trop_i8_selected decide every refusal on the host:
+    CodedMatrix::new's shape rule, the codec fields the decode needs, the
+    triple, and SelectedTriple::new's witness rules.  Fake addresses, never
+    dereferenced."""
+    import uor_gfx950 as u
+    lib = u.lib()
+    P = 0x1000
+    a, c = _v(P, 4 * 48, 4, 48, 48, 1), _v(P, 4 * 16, 4, 16, 16, 1)
+    tern = u.Codec(u.TIER["ternary"], 8, 0, 0, 0, 0, 4, None, 0)  # Ternary<4, u8>
+
+    def coded(cd, codes_len, w_rows=16, w_cols=48, a=a, c=c):
+        return lib.uor_gfx950_gemm_coded(ctypes.byref(a), ctypes.byref(cd), P, codes_len, w_rows,
+                                         w_cols, 1, ctypes.byref(c), 4, 1, 0, 0, None, 0, None, None)
+    assert coded(tern, 16 * 48 // 4 + 1) == 3                       # code count
+    assert coded(tern, 16 * 50 // 4, w_cols=50) == 3                 # width % MAX_BLOCK
+    assert coded(u.Codec(9, 8, 0, 0, 0, 0, 4, None, 0), 192) == 4    # unknown tier
+    assert coded(u.Codec(4, 8, 3, 0, 0, 0, 4, None, 0), 192) == 4    # P = 3
+    assert coded(u.Codec(1, 16, 0, 0, 0, 16, 1, None, 0), 768) == 3  # Grid without its table
+    assert coded(tern, 16 * 40 // 4, w_cols=40) == 1                 # A is 48 deep, W 40
+    assert coded(tern, 192, c=_v(P, 16, 4, 16, 0, 1)) == 2           # aliasing C
+
+    def sel(w, mech=0):
+        av, bv = _v(P, 20, 4, 5, 5, 1), _v(P, 30, 5, 6, 6, 1)
+        cv = _v(P, 24, 4, 6, 6, 1)
+        return lib.uor_gfx950_gemm_trop_i8_selected(ctypes.byref(av), ctypes.byref(bv),
+                                                    ctypes.byref(cv), ctypes.byref(w), 4, 0, 1,
+                                                    0, 0, 0, mech, None, 0, None, None)
+    assert sel(_v(P, 24, 4, 5, 5, 1)) == 1     # witness not m x n
+    assert sel(_v(P, 24, 4, 6, 0, 1)) == 2     # witness aliases itself
+    assert sel(_v(P, 20, 4, 6, 6, 1)) == 3     # witness buffer too short
+    assert sel(_v(P, 24, 4, 6, 6, 1), mech=7) == 4
