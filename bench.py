@@ -369,6 +369,58 @@ def bench_coded(args, torch, uor, gen):
     return runs
 
 
+def bench_collapse(args, torch, uor, gen):
+    """The collapse traversal at the headline's size: m = n = k = 8192, A's
+    rows drawn from 512 distinct rows (a batch of repeated inputs), alpha = 3,
+    beta = 0, i32 out, with the suggested offer; the plain route beside it on
+    the same operands, and the bytes compared."""
+    import numpy as np
+    N, D = 8192, 512
+    dev = torch.device("cuda:0")
+    base = torch.from_numpy(gen.i8_full(D * N, 31)).to(dev).view(D, N)
+    pick = torch.from_numpy((gen.lanes_draws(N, 32) % np.uint64(D)).astype(np.int64)).to(dev)
+    pick[:D] = torch.arange(D, device=dev)
+    a = base[pick].contiguous().view(-1)
+    b = torch.from_numpy(gen.i8_full(N * N, 33)).to(dev)
+    c = torch.zeros(N * N, dtype=torch.int32, device=dev)
+    ref = torch.zeros(N * N, dtype=torch.int32, device=dev)
+    sc = torch.empty(uor.suggested_scratch_collapse(N, N, N), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    route = {}
+
+    def collapsed():
+        st, r = uor.gemm_collapsed_i8(a, (N, N), (N, 1), b, (N, N), (N, 1), c, (N, N), (N, 1),
+                                      alpha=3, scratch=sc, stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"collapsed status {st}")
+        route.update(r)
+
+    def plain():
+        st, _ = uor.gemm_i8(a, (N, N), (N, 1), b, (N, N), (N, 1), ref, (N, N), (N, 1), alpha=3,
+                            stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"plain status {st}")
+
+    def timed(step):
+        step()
+        torch.cuda.synchronize()
+        settle(torch, step)
+        steps = max(1, min(args.steps, 20))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps * 1e3
+
+    # Wall clock per call: the collapse route synchronises on its distinct
+    # count, so stream events would not bracket it any better.
+    ms_c = timed(collapsed)
+    ms_p = timed(plain)
+    return {"m": N, "k": N, "n": N, "distinct_rows": route.get("moduli"), "route": route.get("kind"),
+            "ms_per_call": round(ms_c, 4), "plain_ms_per_call": round(ms_p, 4),
+            "speedup": round(ms_p / ms_c, 2), "bytes_equal_plain": bool(torch.equal(c, ref))}
+
+
 def bench_trop(args, torch, uor, gen):
     """Trop<i8> max-plus GEMM at m = n = k = 4096, 5% of entries
     at the semiring zero, output Trop<i32>.  One term is one (+, max) pair;
@@ -674,6 +726,8 @@ def main():
             "prefill": bench_lut_prefill(args, torch, uor, gen),
             "ternary": bench_coded(args, torch, uor, gen),
         }
+        log("[bench] collapse")
+        result["collapse"] = bench_collapse(args, torch, uor, gen)
     if not args.no_trop:
         log("[bench] trop max-plus")
         result["tropical"] = {

@@ -83,6 +83,7 @@ typedef struct uor_view {
 #define UOR_ROUTE_MFMA_TILE 2     /* int8 MFMA tile, fused epilogue */
 #define UOR_ROUTE_MFMA_SPLITK 3   /* int8 MFMA split-K, exact i64 partials */
 #define UOR_ROUTE_MFMA_WIDE 4     /* int8 MFMA, i64 register widening */
+#define UOR_ROUTE_COLLAPSED 5     /* one product line per distinct line of A (or column of B) */
 #define UOR_ROUTE_LUT4_DOT4 10    /* 4-bit table-lookup, v_perm decode, dot4 (small m) */
 #define UOR_ROUTE_LUT4_MFMA 11    /* 4-bit table-lookup, v_perm decode into int8 MFMA */
 #define UOR_ROUTE_LUT4_PREFILL 12 /* 4-bit table-lookup, many rows: decode W^T, dense int8 MFMA */
@@ -327,6 +328,26 @@ int uor_gfx950_dgemm(uint64_t m, uint64_t k, uint64_t n, int64_t alpha,
  * (replaces suggested_float_panels, float.rs:1876-1882, for this backend). */
 uint64_t uor_gfx950_suggested_scratch_float(int is_f64, uint64_t m, uint64_t k,
                                             uint64_t n);
+
+/*
+ * gemm_collapsed(&mut Triple, &Linear{alpha,beta}, GemmOptions{encode},
+ * &mut Scratch, &mut Collapse) at E = i8 (crates/uor-matmul-gemm/src/
+ * collapse.rs:169-220): the bytes of uor_gfx950_gemm_i8, computing one
+ * output row per distinct row of A (columns = 1: one output column per
+ * distinct column of B, the transposed triple).  beta != 0 (the epilogue
+ * reads C), k = 0, pairwise distinct lines, or an offer smaller than
+ * uor_gfx950_suggested_scratch_collapse bytes run the plain route.  The
+ * route reads back the distinct count (one 4-byte copy, a stream
+ * synchronisation) before the product; route->moduli reports it.
+ */
+int uor_gfx950_gemm_collapsed_i8(const uor_view *a, const uor_view *b, const uor_view *c,
+                                 int out_type, int64_t alpha, int64_t beta, int encode,
+                                 int columns, void *scratch, uint64_t scratch_bytes,
+                                 void *stream, uor_route *route);
+
+/* The offer that lets gemm_collapsed_i8 collapse (suggested_collapse_index
+ * plus suggested_collapse_rows, collapse.rs:103-120, and the product's). */
+uint64_t uor_gfx950_suggested_scratch_collapse(uint64_t m, uint64_t k, uint64_t n);
 
 /* ================================================ (max, +) over Trop<i8> */
 

@@ -22,6 +22,7 @@ ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
           4: "invalid_argument"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
+          5: "collapsed",
           10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill",
           13: "coded_dense", 14: "coded_direct", 15: "coded_gemv", 20: "float_crt", 21: "float_direct", 30: "trop_valu",
           31: "trop_selected", 32: "trop_selected_direct", 40: "int_crt", 41: "int_direct", 42: "int_limb"}
@@ -47,6 +48,8 @@ SYMBOLS = [
     "uor_gfx950_suggested_scratch_float",
     "uor_gfx950_gemm_trop_i8",
     "uor_gfx950_gemm_trop_i8_selected",
+    "uor_gfx950_gemm_collapsed_i8",
+    "uor_gfx950_suggested_scratch_collapse",
 ]
 
 
@@ -124,6 +127,12 @@ def lib():
             L.uor_gfx950_gemm_lut4.restype = _i32
             L.uor_gfx950_suggested_scratch_lut4.argtypes = [_u64, _u64, _u64]
             L.uor_gfx950_suggested_scratch_lut4.restype = _u64
+        if hasattr(L, "uor_gfx950_gemm_collapsed_i8"):
+            L.uor_gfx950_gemm_collapsed_i8.argtypes = [_PV, _PV, _PV, _i32, _i64, _i64, _i32, _i32,
+                                                       _vp, _u64, _vp, _PR]
+            L.uor_gfx950_gemm_collapsed_i8.restype = _i32
+            L.uor_gfx950_suggested_scratch_collapse.argtypes = [_u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_collapse.restype = _u64
         if hasattr(L, "uor_gfx950_gemm_coded"):
             L.uor_gfx950_gemm_coded.argtypes = [_PV, ctypes.POINTER(Codec), _vp, _u64, _u64, _u64,
                                                 _i32, _PV, _i32, _i64, _i64, _i32, _vp, _u64, _vp,
@@ -364,3 +373,25 @@ def gemm_coded(a, a_shape, a_strides, cd, codes, w_rows, w_cols, transposed, c, 
 
 def suggested_scratch_coded(m, k, n):
     return lib().uor_gfx950_suggested_scratch_coded(m, k, n)
+
+
+def gemm_collapsed_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+                      out="i32", alpha=1, beta=0, encode="nearest", columns=False, scratch=None,
+                      stream=None):
+    """gemm_collapsed at E = i8: the bytes of gemm_i8, one product line per
+    distinct row of A (columns=True: per distinct column of B)."""
+    ob = OUT[out]
+    av = view(a, *a_shape, *a_strides)
+    bv = view(b, *b_shape, *b_strides)
+    cv = view(c, *c_shape, *c_strides, rec=2 if ob == 16 else 1)
+    r = Route()
+    st = lib().uor_gfx950_gemm_collapsed_i8(
+        ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob, int(alpha), int(beta),
+        ENCODE[encode], int(bool(columns)), _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def suggested_scratch_collapse(m, k, n):
+    return lib().uor_gfx950_suggested_scratch_collapse(m, k, n)
