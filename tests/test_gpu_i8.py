@@ -403,3 +403,23 @@ def test_splitk_narrow_tile_folds_segments(uor, dev):
     assert st == 0 and route["tile_m"] == 32, route
     S = (a.view(m, k).double() @ b.view(k, n).double()).cpu().numpy().astype(np.int64)
     assert np.array_equal(c.cpu().numpy().reshape(m, n), S)
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 1024, 28672), (256, 2048, 28672), (300, 640, 20000)])
+@pytest.mark.parametrize("out", ["i32", "i64"])
+def test_wide_tile_below_one_round(uor, dev, m, k, n, out):
+    """Fewer 256-wide tiles than CUs, wide n: the 256-wide tile (one round)
+    rather than several rounds of 128-wide tiles; ragged edges included.
+    Checked in float64 on the device (|3 AB - C| < 2^53)."""
+    g = torch.Generator(device=dev).manual_seed(m + n)
+    a = torch.randint(-128, 128, (m * k,), dtype=torch.int8, device=dev, generator=g)
+    b = torch.randint(-128, 128, (k * n,), dtype=torch.int8, device=dev, generator=g)
+    dt = torch.int32 if out == "i32" else torch.int64
+    c0 = torch.randint(-(1 << 20), 1 << 20, (m * n,), dtype=dt, device=dev, generator=g)
+    c = c0.clone()
+    st, route = uor.gemm_i8(a, (m, k), (k, 1), b, (k, n), (n, 1), c, (m, n), (n, 1), out=out,
+                            alpha=3, beta=-1)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == 256, route
+    want = 3 * (a.view(m, k).double() @ b.view(k, n).double()) - c0.view(m, n).double()
+    assert torch.equal(c.view(m, n).double(), want)

@@ -1254,8 +1254,14 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         }
         return UOR_OK;
     }
+    // The 256-wide tile also below one tile per CU: at k = 8192 it ran
+    // m = 512, n = 28672 (224 tiles) in 0.138 ms, m = 256 in 0.086 ms and
+    // m = 128 in 0.080 ms, where the 128-wide tile took 0.337, 0.155 and
+    // 0.136 ms (1024 x 4096 x 4096: 0.047 against 0.074 ms).  At 16 tiles the
+    // two are even (512 x 2048 x 2048: 0.030 against 0.026 ms), hence 32.
+    const bool use256 = t256 >= 256 || (M >= 128 && N >= 128 && t256 >= 32);
     int bm;
-    if (t256 >= 256 && dl_ok(pair, K, N)) {
+    if (use256 && dl_ok(pair, K, N)) {
         bm = 256;
         const int v = dl_variant();
         if (v == DL_S4 && s4_ok(A, B)) {
@@ -1266,7 +1272,7 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         default: UOR_HIP((launch_dl<256, 256, 2, 4, EPI_FUSED, FAST, false>(A, B, out, K, 0, 1, s))); break;
         }
         if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline
-    } else if (FAST && t256 >= 256 && pair != 4) {
+    } else if (FAST && use256 && pair != 4) {
         // (The i128 epilogue does not fit beside a 256-wide generic tile's
         // registers; those requests take the 128-wide tile below.)
         bm = 256;
