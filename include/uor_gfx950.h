@@ -278,6 +278,26 @@ int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, const void 
 /* The offer that lets gemm_coded take the decode-then-dense route. */
 uint64_t uor_gfx950_suggested_scratch_coded(uint64_t m, uint64_t k, uint64_t n);
 
+/*
+ * The same product with the row collapse gemm_tabulated takes as its
+ * `collapse` argument (tabulated.rs:2555-2660, collapse.rs:71-120): with
+ * beta = 0 and an offer of uor_gfx950_suggested_scratch_coded_collapse
+ * bytes, equal rows of A share one product row (the pass reads back the
+ * distinct count: a stream synchronisation; route->kind is
+ * UOR_ROUTE_COLLAPSED and route->moduli the count).  Otherwise, or when
+ * every row is distinct, it is uor_gfx950_gemm_coded.  The bytes are the
+ * same (CD-15).
+ */
+int uor_gfx950_gemm_coded_collapsed(const uor_view *a, const uor_codec *codec,
+                                    const void *codes, uint64_t codes_len, uint64_t w_rows,
+                                    uint64_t w_cols, int transposed, const uor_view *c,
+                                    int out_type, int64_t alpha, int64_t beta, int encode,
+                                    void *scratch, uint64_t scratch_bytes, void *stream,
+                                    uor_route *route);
+
+/* The offer that lets gemm_coded_collapsed collapse. */
+uint64_t uor_gfx950_suggested_scratch_coded_collapse(uint64_t m, uint64_t k, uint64_t n);
+
 /* =================================================== exact float GEMM */
 
 /*

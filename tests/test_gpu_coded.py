@@ -252,3 +252,50 @@ def test_four_bit_codec_equals_lut4(uor, dev):
         assert st == 0
         torch.cuda.synchronize()
         assert torch.equal(c1, c2), offer
+
+
+@pytest.mark.parametrize("name", ["ternary4_u8", "packed_grid16_p2", "book256x8", "sign12_u8"])
+@pytest.mark.parametrize("transposed", [True, False])
+@pytest.mark.parametrize("m,distinct", [(40, 4), (300, 20)])
+def test_row_collapse(oracle, uor, dev, name, transposed, m, distinct):
+    """gemm_coded_collapsed: A's rows drawn from a few distinct ones share
+    product rows (the inner product then runs on d rows: the register route
+    at d <= 8 for W n x k); the bytes are the oracle's and the plain coded
+    route's.  beta != 0 and no offer run the plain routes."""
+    spec = SPECS[name]
+    rng = np.random.default_rng(m + len(name))
+    k, n = 96, 48
+    rows, cols = (n, k) if transposed else (k, n)
+    mb = max_block(spec)
+    wide = not spec.get("packed") and spec.get("code_bits", 16) == 16
+    codes = rng.integers(0, 1 << 16 if wide else 1 << 8, rows * cols // mb).astype(
+        np.uint16 if wide else np.uint8)
+    base = rng.integers(-128, 128, (distinct, k)).astype(np.int8)
+    pick = rng.integers(0, distinct, m)
+    pick[:distinct] = np.arange(distinct)
+    a = base[pick].reshape(-1).copy()
+    kw = {x: spec[x] for x in ("code_bits", "packed", "zero", "block") if x in spec}
+    table = spec.get("table")
+    gtable = None if table is None else torch.from_numpy(table).to(dev)
+    gcd = uor.codec(spec["tier"], table=gtable, **kw)
+    gcodes = torch.from_numpy(codes.view(np.int16) if wide else codes).to(dev)
+    ga = torch.from_numpy(a).to(dev)
+    for beta, offer, want_kind in ((0, True, "collapsed"), (2, True, None), (0, False, None)):
+        c0 = rng.integers(-1000, 1000, m * n).astype(np.int32)
+        want = c0.copy()
+        ocd = oracle.codec(spec["tier"], table=table, **kw)
+        assert oracle.gemm_coded(a, (m, k), (k, 1), ocd, codes, rows, cols, transposed, want,
+                                 (m, n), (n, 1), alpha=-3, beta=beta) == "ok"
+        gc = torch.from_numpy(c0.copy()).to(dev)
+        nb = uor.suggested_scratch_coded_collapse(m, k, n) if offer else 0
+        scratch = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
+        st, route = uor.gemm_coded(ga, (m, k), (k, 1), gcd, gcodes, rows, cols, transposed, gc,
+                                   (m, n), (n, 1), alpha=-3, beta=beta, scratch=scratch,
+                                   collapse=True)
+        torch.cuda.synchronize()
+        assert st == 0
+        assert np.array_equal(gc.cpu().numpy(), want), (beta, offer, route)
+        if want_kind:
+            assert route["kind"] == want_kind and route["moduli"] == distinct, route
+        else:
+            assert route["kind"] != "collapsed", route

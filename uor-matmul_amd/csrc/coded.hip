@@ -16,6 +16,7 @@
 // output cell decodes its column as it sums.  Both give the same bytes.
 
 #include "common.hpp"
+#include "collapse.hpp"
 
 extern "C" int uor_gfx950_gemm_i8(const uor_view *a, const uor_view *b, const uor_view *c, int out_type,
                                   int64_t alpha, int64_t beta, int encode, void *scratch,
@@ -644,10 +645,37 @@ extern "C" uint64_t uor_gfx950_suggested_scratch_coded(uint64_t m, uint64_t k, u
     return decoded_bytes(k, n) + uor_gfx950_suggested_scratch_i8(m, k, n);
 }
 
+static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void *codes, uint64_t codes_len,
+                           uint64_t w_rows, uint64_t w_cols, int transposed, const uor_view *c, int out_type,
+                           int64_t alpha, int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
+                           void *stream, uor_route *route, bool collapse);
+
 extern "C" int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, const void *codes,
                                      uint64_t codes_len, uint64_t w_rows, uint64_t w_cols, int transposed,
                                      const uor_view *c, int out_type, int64_t alpha, int64_t beta, int encode,
                                      void *scratch, uint64_t scratch_bytes, void *stream, uor_route *route) {
+    return gemm_coded_impl(a, codec, codes, codes_len, w_rows, w_cols, transposed, c, out_type, alpha, beta, encode,
+                           scratch, scratch_bytes, stream, route, false);
+}
+
+extern "C" int uor_gfx950_gemm_coded_collapsed(const uor_view *a, const uor_codec *codec, const void *codes,
+                                               uint64_t codes_len, uint64_t w_rows, uint64_t w_cols, int transposed,
+                                               const uor_view *c, int out_type, int64_t alpha, int64_t beta,
+                                               int encode, void *scratch, uint64_t scratch_bytes, void *stream,
+                                               uor_route *route) {
+    return gemm_coded_impl(a, codec, codes, codes_len, w_rows, w_cols, transposed, c, out_type, alpha, beta, encode,
+                           scratch, scratch_bytes, stream, route, true);
+}
+
+extern "C" uint64_t uor_gfx950_suggested_scratch_coded_collapse(uint64_t m, uint64_t k, uint64_t n) {
+    if (m == 0 || n == 0 || k == 0 || m > 0xFFFFFFFEull) return 0;
+    return collapse_layout(m, k, n, 16).rest + uor_gfx950_suggested_scratch_coded(m, k, n) + 256;
+}
+
+static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void *codes, uint64_t codes_len,
+                           uint64_t w_rows, uint64_t w_cols, int transposed, const uor_view *c, int out_type,
+                           int64_t alpha, int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
+                           void *stream, uor_route *route, bool collapse) {
     route_set(route, UOR_ROUTE_NONE);
     if (!valid_out_type(out_type) || !valid_encode(encode)) return UOR_INVALID_ARGUMENT;
     CodedArgs W{};
@@ -676,6 +704,41 @@ extern "C" int uor_gfx950_gemm_coded(const uor_view *a, const uor_codec *codec, 
     if ((uintptr_t)C.base % (uint64_t)(out_type > 8 ? 8 : out_type)) return UOR_INVALID_ARGUMENT;
     const uint64_t m = A.rows;
     hipStream_t s = (hipStream_t)stream;
+
+    // The row collapse (tabulated.rs:2627-2660, collapse.rs): with beta = 0
+    // and room for the pass, equal rows of A share one product row.
+    if (collapse && beta == 0 && k > 0 && m > 1 && m <= 0xFFFFFFFEull && (m + 3) / 4 <= 0x7FFFFFFFull &&
+        ((uintptr_t)C.base % (uintptr_t)(out_type < 8 ? out_type : 8)) == 0) {
+        const CollapseLayout CL = collapse_layout(m, k, n, out_type);
+        const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+        const uint64_t have = scratch && scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
+        if (have >= CL.rest) {
+            char *sc = (char *)p1;
+            const RowsArgs R{(const int8_t *)A.base, A.rs, A.cs, m, k};
+            uint32_t d = 0;
+            if ((st = collapse_pass(R, sc, CL, s, &d))) return st;
+            if (d < m) {
+                const uor_view cav{sc + CL.compact, (uint64_t)d * CL.ldc, d, k, (int64_t)CL.ldc, 1};
+                const uor_view pv{sc + CL.prod, (uint64_t)d * n, d, n, (int64_t)n, 1};
+                uor_route r{};
+                st = gemm_coded_impl(&cav, codec, codes, codes_len, w_rows, w_cols, transposed, &pv, out_type, alpha,
+                                     0, encode, sc + CL.rest, have - CL.rest, stream, &r, false);
+                if (st) return st;
+                if ((st = collapse_expand(sc + CL.prod, (const uint32_t *)(sc + CL.index), m, n, C.base, C.rs, C.cs,
+                                          out_type, s)))
+                    return st;
+                if (route) {
+                    *route = r;
+                    route->kind = UOR_ROUTE_COLLAPSED;
+                    route->moduli = (int)d;  // distinct rows
+                    route->launches = r.launches + 6;
+                    route->scratch_used = CL.rest + r.scratch_used;
+                }
+                return UOR_OK;
+            }
+            // Pairwise distinct rows: the routes below, having paid the pass.
+        }
+    }
 
     if (transposed && k > 0 && m <= 8 && k <= GEMV_MAX_K && (n + 3) / 4 <= 0x7FFFFFFFull) {
         const bool a_vec = A.cs == 1 && A.rs > 0 && (A.rs % 16) == 0 && ((uintptr_t)A.base & 15) == 0;

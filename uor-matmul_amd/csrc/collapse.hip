@@ -24,6 +24,7 @@
 // copies row index[i] of that buffer to row i of C.
 
 #include "common.hpp"
+#include "collapse.hpp"
 
 extern "C" int uor_gfx950_gemm_i8(const uor_view *a, const uor_view *b, const uor_view *c, int out_type,
                                   int64_t alpha, int64_t beta, int encode, void *scratch,
@@ -32,11 +33,7 @@ extern "C" uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint
 
 namespace uor {
 
-struct RowsArgs {
-    const int8_t *a;  // element (0,0)
-    int64_t rs, cs;
-    uint64_t m, k;
-};
+
 
 __device__ inline uint64_t mix64(uint64_t z) {
     // splitmix64's finaliser (Steele, Lea, Flood 2014).
@@ -165,10 +162,7 @@ __global__ void __launch_bounds__(256) expand16_kernel(const char *P, uint64_t r
         *(uint4 *)(c + (int64_t)i * crs_bytes + (int64_t)q) = *(const uint4 *)(P + (uint64_t)index[i] * row_bytes + q);
 }
 
-struct CollapseLayout {
-    uint64_t hash, key, row, rep, id, index, counter, compact, prod, rest;
-    uint64_t slots, ldc;
-};
+
 
 static uint64_t up256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
 
@@ -178,7 +172,7 @@ static uint64_t next_pow2(uint64_t x) {
     return p;
 }
 
-static CollapseLayout collapse_layout(uint64_t m, uint64_t k, uint64_t n, int ob) {
+CollapseLayout collapse_layout(uint64_t m, uint64_t k, uint64_t n, int ob) {
     CollapseLayout L{};
     L.slots = next_pow2(2 * m);
     L.ldc = (k + 15) / 16 * 16;
@@ -193,6 +187,49 @@ static CollapseLayout collapse_layout(uint64_t m, uint64_t k, uint64_t n, int ob
     L.prod = L.compact + up256(m * L.ldc);
     L.rest = L.prod + up256(m * n * (uint64_t)ob);
     return L;
+}
+
+// The pass over the m lines of R: their classes, the compacted distinct
+// lines (d x ldc at `compact`) and every line's class number (`index`),
+// then the count d read back to the host.  Buffers in `sc` by `L`.
+int collapse_pass(const RowsArgs &R, char *sc, const CollapseLayout &L, hipStream_t s, uint32_t *d_out) {
+    const uint64_t m = R.m;
+    uint64_t *hash = (uint64_t *)(sc + L.hash);
+    unsigned long long *key = (unsigned long long *)(sc + L.key);
+    uint32_t *row = (uint32_t *)(sc + L.row), *rep = (uint32_t *)(sc + L.rep), *id = (uint32_t *)(sc + L.id);
+    uint32_t *index = (uint32_t *)(sc + L.index), *counter = (uint32_t *)(sc + L.counter);
+    int8_t *compact = (int8_t *)(sc + L.compact);
+    const unsigned wgrid = (unsigned)((m + 3) / 4);
+    hipLaunchKernelGGL(row_hash_kernel, dim3(wgrid), dim3(256), 0, s, R, hash);
+    hipLaunchKernelGGL(table_clear_kernel, dim3((unsigned)((L.slots + 255) / 256)), dim3(256), 0, s, key, row,
+                       L.slots, counter);
+    hipLaunchKernelGGL(table_insert_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, hash, m, key, row,
+                       L.slots - 1);
+    hipLaunchKernelGGL(class_kernel, dim3(wgrid), dim3(256), 0, s, R, hash, key, row, L.slots - 1, rep, id, counter,
+                       compact, L.ldc);
+    hipLaunchKernelGGL(index_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, m, rep, id, index);
+    UOR_HIP(hipGetLastError());
+    uint32_t d = 0;
+    UOR_HIP(hipMemcpyAsync(&d, counter, 4, hipMemcpyDeviceToHost, s));
+    UOR_HIP(hipStreamSynchronize(s));
+    if (d == 0 || d > m) return UOR_HIP_ERROR;
+    *d_out = d;
+    return UOR_OK;
+}
+
+// C[i, j] := P[index[i], j] for the m x n output (ob-byte elements).
+int collapse_expand(const char *P, const uint32_t *index, uint64_t m, uint64_t n, char *c, int64_t crs, int64_t ccs,
+                    int ob, hipStream_t s) {
+    const unsigned gy = (unsigned)(m < 65535 ? m : 65535);
+    const uint64_t row_bytes = n * (uint64_t)ob;
+    if (ccs == 1 && row_bytes % 16 == 0 && ((uintptr_t)c & 15) == 0 && ((crs * ob) % 16) == 0)
+        hipLaunchKernelGGL(expand16_kernel, dim3((unsigned)((row_bytes / 16 + 255) / 256), gy), dim3(256), 0, s, P,
+                           row_bytes, index, m, c, crs * (int64_t)ob);
+    else
+        hipLaunchKernelGGL(expand_kernel, dim3((unsigned)((n + 255) / 256), gy), dim3(256), 0, s, P, n, index, m, c,
+                           crs, ccs, ob);
+    UOR_HIP(hipGetLastError());
+    return UOR_OK;
 }
 
 }  // namespace uor
@@ -251,27 +288,12 @@ extern "C" int uor_gfx950_gemm_collapsed_i8(const uor_view *a, const uor_view *b
     if (have < L.rest) return plain();
     char *sc = (char *)p1;
     hipStream_t s = (hipStream_t)stream;
-    uint64_t *hash = (uint64_t *)(sc + L.hash);
-    unsigned long long *key = (unsigned long long *)(sc + L.key);
-    uint32_t *row = (uint32_t *)(sc + L.row), *rep = (uint32_t *)(sc + L.rep), *id = (uint32_t *)(sc + L.id);
-    uint32_t *index = (uint32_t *)(sc + L.index), *counter = (uint32_t *)(sc + L.counter);
+    uint32_t *index = (uint32_t *)(sc + L.index);
     int8_t *compact = (int8_t *)(sc + L.compact);
     char *prod = sc + L.prod;
-    const unsigned wgrid = (unsigned)((m + 3) / 4);
-    hipLaunchKernelGGL(row_hash_kernel, dim3(wgrid), dim3(256), 0, s, R, hash);
-    hipLaunchKernelGGL(table_clear_kernel, dim3((unsigned)((L.slots + 255) / 256)), dim3(256), 0, s, key, row,
-                       L.slots, counter);
-    hipLaunchKernelGGL(table_insert_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, hash, m, key, row,
-                       L.slots - 1);
-    hipLaunchKernelGGL(class_kernel, dim3(wgrid), dim3(256), 0, s, R, hash, key, row, L.slots - 1, rep, id, counter,
-                       compact, L.ldc);
-    hipLaunchKernelGGL(index_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, m, rep, id, index);
-    UOR_HIP(hipGetLastError());
     // The count of distinct rows decides the product's size.
     uint32_t d = 0;
-    UOR_HIP(hipMemcpyAsync(&d, counter, 4, hipMemcpyDeviceToHost, s));
-    UOR_HIP(hipStreamSynchronize(s));
-    if (d == 0 || d > m) return UOR_HIP_ERROR;
+    if ((st = collapse_pass(R, sc, L, s, &d))) return st;
     // Pairwise distinct lines: the plain route, having paid the pass.
     if (d == m) return plain();
     // The distinct lines' product, with the caller's scalars and encode, into
@@ -281,15 +303,7 @@ extern "C" int uor_gfx950_gemm_collapsed_i8(const uor_view *a, const uor_view *b
     uor_route r{};
     st = uor_gfx950_gemm_i8(&cav, &bv, &pv, out_type, alpha, 0, encode, sc + L.rest, have - L.rest, stream, &r);
     if (st) return st;
-    const unsigned gy = (unsigned)(m < 65535 ? m : 65535);
-    const uint64_t row_bytes = n * (uint64_t)ob;
-    if (ccs == 1 && row_bytes % 16 == 0 && ((uintptr_t)C.base & 15) == 0 && ((crs * ob) % 16) == 0)
-        hipLaunchKernelGGL(expand16_kernel, dim3((unsigned)((row_bytes / 16 + 255) / 256), gy), dim3(256), 0, s, prod,
-                           row_bytes, index, m, C.base, crs * (int64_t)ob);
-    else
-        hipLaunchKernelGGL(expand_kernel, dim3((unsigned)((n + 255) / 256), gy), dim3(256), 0, s, prod, n, index, m,
-                           C.base, crs, ccs, ob);
-    UOR_HIP(hipGetLastError());
+    if ((st = collapse_expand(prod, index, m, n, C.base, crs, ccs, ob, s))) return st;
     if (route) {
         *route = r;
         route->kind = UOR_ROUTE_COLLAPSED;

@@ -41,6 +41,8 @@ SYMBOLS = [
     "uor_gfx950_suggested_scratch_lut4",
     "uor_gfx950_gemm_coded",
     "uor_gfx950_suggested_scratch_coded",
+    "uor_gfx950_gemm_coded_collapsed",
+    "uor_gfx950_suggested_scratch_coded_collapse",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
     "uor_gfx950_sgemm",
@@ -140,6 +142,10 @@ def lib():
             L.uor_gfx950_gemm_coded.restype = _i32
             L.uor_gfx950_suggested_scratch_coded.argtypes = [_u64, _u64, _u64]
             L.uor_gfx950_suggested_scratch_coded.restype = _u64
+            L.uor_gfx950_gemm_coded_collapsed.argtypes = L.uor_gfx950_gemm_coded.argtypes
+            L.uor_gfx950_gemm_coded_collapsed.restype = _i32
+            L.uor_gfx950_suggested_scratch_coded_collapse.argtypes = [_u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_coded_collapse.restype = _u64
         if hasattr(L, "uor_gfx950_gemm_float"):
             L.uor_gfx950_gemm_float.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32, _vp, _u64,
                                                 _vp, _PR]
@@ -354,7 +360,7 @@ def codec(tier, code_bits=16, packed=0, zero=None, table=None, entries=None, blo
 
 def gemm_coded(a, a_shape, a_strides, cd, codes, w_rows, w_cols, transposed, c, c_shape,
                c_strides, out="i32", alpha=1, beta=0, encode="nearest", scratch=None,
-               stream=None):
+               stream=None, collapse=False):
     """gemm_tabulated (transposed: W is n x k) or coded_gemm (W is k x n) with
     W a fixed-width coded operand: `codes` is a device tensor of the stored
     codes (uint8, or int16/uint16 for 16-bit codes)."""
@@ -363,7 +369,8 @@ def gemm_coded(a, a_shape, a_strides, cd, codes, w_rows, w_cols, transposed, c, 
     av = view(a, *a_shape, *a_strides)
     cv = view(c, *c_shape, *c_strides, rec=rec)
     r = Route()
-    st = lib().uor_gfx950_gemm_coded(
+    f = lib().uor_gfx950_gemm_coded_collapsed if collapse else lib().uor_gfx950_gemm_coded
+    st = f(
         ctypes.byref(av), ctypes.byref(cd), _ptr(codes), codes.numel(), w_rows, w_cols,
         int(bool(transposed)), ctypes.byref(cv), ob, int(alpha), int(beta), ENCODE[encode],
         _ptr(scratch), 0 if scratch is None else scratch.numel() * scratch.element_size(),
@@ -395,3 +402,7 @@ def gemm_collapsed_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, 
 
 def suggested_scratch_collapse(m, k, n):
     return lib().uor_gfx950_suggested_scratch_collapse(m, k, n)
+
+
+def suggested_scratch_coded_collapse(m, k, n):
+    return lib().uor_gfx950_suggested_scratch_coded_collapse(m, k, n)
