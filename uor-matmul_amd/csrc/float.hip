@@ -1881,22 +1881,50 @@ __global__ void __launch_bounds__(256) limb_split_a_kernel(IArgs F, int8_t *acat
     if (threadIdx.x == 0) atomicAdd((unsigned long long *)&sa[i], (unsigned long long)(part[0] + part[1] + part[2] + part[3]));
 }
 
-// Thread: column j, LIMB_SPLIT_B consecutive rows of B.
-template <int EB>
+// Thread: column j (VEC4: columns 4j .. 4j + 3, one 4-byte store per limb
+// plane and row), LIMB_SPLIT_B consecutive rows of B.
+template <int EB, bool VEC4>
 __global__ void __launch_bounds__(256) limb_split_b_kernel(IArgs F, int8_t *brev, int64_t *sb) {
     constexpr int L = EB;
-    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    constexpr int NJ = VEC4 ? 4 : 1;
+    const uint64_t j = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * NJ;
     const uint64_t p0 = (uint64_t)blockIdx.y * LIMB_SPLIT_B;
     if (j >= F.n) return;
-    int64_t sum = 0;
+    int64_t sum[NJ];
+#pragma unroll
+    for (int q = 0; q < NJ; ++q) sum[q] = 0;
     for (int e = 0; e < LIMB_SPLIT_B && p0 + e < F.k; ++e) {
         const uint64_t p = p0 + e;
-        const int64_t v = load_ielem<EB>(F.b, (int64_t)p * F.brs + (int64_t)j * F.bcs);
-        sum += v;
+        int64_t v[NJ];
+        if constexpr (VEC4) {
+            const char *src = F.b + ((int64_t)p * F.brs + (int64_t)j) * EB;
+            if constexpr (EB == 2) {
+                const uint2 x = *(const uint2 *)src;
+                v[0] = (int16_t)x.x, v[1] = (int16_t)(x.x >> 16), v[2] = (int16_t)x.y, v[3] = (int16_t)(x.y >> 16);
+            } else {
+                const uint4 x = *(const uint4 *)src;
+                v[0] = (int32_t)x.x, v[1] = (int32_t)x.y, v[2] = (int32_t)x.z, v[3] = (int32_t)x.w;
+            }
+        } else {
+            v[0] = load_ielem<EB>(F.b, (int64_t)p * F.brs + (int64_t)j * F.bcs);
+        }
 #pragma unroll
-        for (int t = 0; t < L; ++t) brev[((uint64_t)(L - 1 - t) * F.k + p) * F.n + j] = limb_of<EB>(v, t);
+        for (int q = 0; q < NJ; ++q) sum[q] += v[q];
+#pragma unroll
+        for (int t = 0; t < L; ++t) {
+            int8_t *dst = brev + ((uint64_t)(L - 1 - t) * F.k + p) * F.n + j;
+            if constexpr (VEC4) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) w |= (uint32_t)(uint8_t)limb_of<EB>(v[q], t) << (8 * q);
+                *(uint32_t *)dst = w;
+            } else {
+                *dst = limb_of<EB>(v[0], t);
+            }
+        }
     }
-    atomicAdd((unsigned long long *)&sb[j], (unsigned long long)sum);
+#pragma unroll
+    for (int q = 0; q < NJ; ++q) atomicAdd((unsigned long long *)&sb[j + q], (unsigned long long)sum[q]);
 }
 
 // One thread per cell: X from the planes and the line sums (two's-complement
@@ -1973,9 +2001,17 @@ static int launch_int_limb(const IArgs &F, char *sc, uint64_t have, const LimbLa
     hipLaunchKernelGGL(limb_split_a_kernel<EB>,
                        dim3((unsigned)((k + 256 * LIMB_SPLIT_A - 1) / (256 * LIMB_SPLIT_A)), (unsigned)m), dim3(256),
                        0, s, F, acat, sa);
-    hipLaunchKernelGGL(limb_split_b_kernel<EB>,
-                       dim3((unsigned)((n + 255) / 256), (unsigned)((k + LIMB_SPLIT_B - 1) / LIMB_SPLIT_B)), dim3(256),
-                       0, s, F, brev, sb);
+    // Four columns per thread when B's rows are contiguous, n is a multiple
+    // of 4 and every row starts 4-element aligned.
+    const bool vec4 = F.bcs == 1 && n % 4 == 0 && F.brs % 4 == 0 && ((uintptr_t)F.b % (4 * EB)) == 0;
+    if (vec4)
+        hipLaunchKernelGGL((limb_split_b_kernel<EB, true>),
+                           dim3((unsigned)((n / 4 + 255) / 256), (unsigned)((k + LIMB_SPLIT_B - 1) / LIMB_SPLIT_B)),
+                           dim3(256), 0, s, F, brev, sb);
+    else
+        hipLaunchKernelGGL((limb_split_b_kernel<EB, false>),
+                           dim3((unsigned)((n + 255) / 256), (unsigned)((k + LIMB_SPLIT_B - 1) / LIMB_SPLIT_B)),
+                           dim3(256), 0, s, F, brev, sb);
     UOR_HIP(hipGetLastError());
     *launches = 4;
     for (int sft = 0; sft < Y.nplanes; ++sft) {
