@@ -299,3 +299,30 @@ def test_row_collapse(oracle, uor, dev, name, transposed, m, distinct):
             assert route["kind"] == want_kind and route["moduli"] == distinct, route
         else:
             assert route["kind"] != "collapsed", route
+
+
+@pytest.mark.parametrize("transposed", [True, False])
+def test_dense_route_strided_a(oracle, uor, dev, transposed):
+    """The decode-into-scratch route hands the caller's A view to the dense
+    int8 route as it is: column-major, padded and reversed rows."""
+    spec = SPECS["ternary4_u8"]
+    rng = np.random.default_rng(17)
+    m, k, n = 20, 128, 64
+    rows, cols = (n, k) if transposed else (k, n)
+    codes = rng.integers(0, 256, rows * cols // 4).astype(np.uint8)
+    ocd = oracle.codec("ternary", code_bits=8, block=4)
+    gcd = uor.codec("ternary", code_bits=8, block=4)
+    for a_str, alen in (((1, m), m * k), ((k + 8, 1), m * (k + 8)), ((-k, 1), m * k)):
+        a = rng.integers(-128, 128, alen).astype(np.int8)
+        c0 = rng.integers(-1000, 1000, m * n).astype(np.int32)
+        want = c0.copy()
+        assert oracle.gemm_coded(a, (m, k), a_str, ocd, codes, rows, cols, transposed, want,
+                                 (m, n), (n, 1), alpha=5, beta=-1) == "ok"
+        gc = torch.from_numpy(c0.copy()).to(dev)
+        sc = torch.empty(uor.suggested_scratch_coded(m, k, n), dtype=torch.uint8, device=dev)
+        st, route = uor.gemm_coded(torch.from_numpy(a).to(dev), (m, k), a_str, gcd,
+                                   torch.from_numpy(codes).to(dev), rows, cols, transposed, gc,
+                                   (m, n), (n, 1), alpha=5, beta=-1, scratch=sc)
+        torch.cuda.synchronize()
+        assert st == 0 and route["kind"] == "coded_dense", route
+        assert np.array_equal(gc.cpu().numpy(), want), a_str
