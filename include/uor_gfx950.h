@@ -298,6 +298,28 @@ int uor_gfx950_gemm_coded_collapsed(const uor_view *a, const uor_codec *codec,
 /* The offer that lets gemm_coded_collapsed collapse. */
 uint64_t uor_gfx950_suggested_scratch_coded_collapse(uint64_t m, uint64_t k, uint64_t n);
 
+/*
+ * A float product with an Arena-coded operand (Arena<f32|f64, N, u8|u16>,
+ * crates/uor-matmul-codec/src/codecs.rs:894-960, CK-14): element (r, q) of
+ * the w_rows x w_cols coded matrix is table[code(r, q) % entries], the codes
+ * row-major, one per element (MAX_BLOCK 1).  transposed = 1: W is n x k
+ * (C := A W^T); 0: W is k x n.  a, c: views of f32 (is_f64 = 0) or f64;
+ * table: `entries` device values of that type.  The operand is decoded once
+ * into the scratch, then multiplied by uor_gfx950_gemm_float (exact, one
+ * rounding), so the bytes are those of the dense spelling's product.  There
+ * is no decode-free route: an offer below the decoded operand's k*n*size
+ * bytes is UOR_INVALID_ARGUMENT; uor_gfx950_suggested_scratch_coded_float
+ * adds the float route's own offer.
+ */
+int uor_gfx950_gemm_coded_float(int is_f64, const uor_view *a, const void *table,
+                                uint64_t entries, int code_bits, const void *codes,
+                                uint64_t codes_len, uint64_t w_rows, uint64_t w_cols,
+                                int transposed, const uor_view *c, int64_t alpha, int64_t beta,
+                                int encode, void *scratch, uint64_t scratch_bytes, void *stream,
+                                uor_route *route);
+
+uint64_t uor_gfx950_suggested_scratch_coded_float(int is_f64, uint64_t m, uint64_t k, uint64_t n);
+
 /* =================================================== exact float GEMM */
 
 /*

@@ -821,3 +821,83 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
     }
     return UOR_OK;
 }
+
+// ------------------------------------------------------------ Arena tier --
+//
+// Arena<E, N, K> over f32 / f64 (codecs.rs:894-960): a one-element block
+// whose decode is table[code % N], the table an artifact's distinct bit
+// patterns.  The coded operand is decoded once into the scratch as a k x n
+// matrix of E, then the exact float route multiplies it (the decode carries
+// bit patterns, so the product is the float product of the dense spelling).
+
+template <typename T>
+__global__ void __launch_bounds__(256) arena_decode_kernel(const T *table, uint64_t entries, const uint8_t *codes,
+                                                           int cb, uint64_t w_cols, int trans, uint64_t k,
+                                                           uint64_t n, T *out) {
+    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= n) return;
+    for (uint64_t p = blockIdx.y; p < k; p += gridDim.y) {
+        const uint64_t at = trans ? j * w_cols + p : p * w_cols + j;
+        const uint32_t code = cb == 1 ? (uint32_t)codes[at] : (uint32_t)((const uint16_t *)codes)[at];
+        out[p * n + j] = table[code % entries];
+    }
+}
+
+extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_view *b, const uor_view *c,
+                                     int64_t alpha, int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
+                                     void *stream, uor_route *route);
+extern "C" uint64_t uor_gfx950_suggested_scratch_float(int is_f64, uint64_t m, uint64_t k, uint64_t n);
+
+extern "C" uint64_t uor_gfx950_suggested_scratch_coded_float(int is_f64, uint64_t m, uint64_t k, uint64_t n) {
+    if (m == 0 || n == 0 || k == 0) return 0;
+    return round_up(k * n * (is_f64 ? 8 : 4), 256) + uor_gfx950_suggested_scratch_float(is_f64, m, k, n);
+}
+
+extern "C" int uor_gfx950_gemm_coded_float(int is_f64, const uor_view *a, const void *table, uint64_t entries,
+                                           int code_bits, const void *codes, uint64_t codes_len, uint64_t w_rows,
+                                           uint64_t w_cols, int transposed, const uor_view *c, int64_t alpha,
+                                           int64_t beta, int encode, void *scratch, uint64_t scratch_bytes,
+                                           void *stream, uor_route *route) {
+    route_set(route, UOR_ROUTE_NONE);
+    if (!(is_f64 == 0 || is_f64 == 1) || !(code_bits == 8 || code_bits == 16) || !valid_encode(encode))
+        return UOR_INVALID_ARGUMENT;
+    if (entries == 0 || !table) return UOR_INVALID_ARGUMENT;
+    const int eb = is_f64 ? 8 : 4;
+    // CodedMatrix::new at MAX_BLOCK 1 (matrix.rs:36-55).
+    uint64_t ncodes;
+    if (__builtin_mul_overflow(w_rows, w_cols, &ncodes) || ncodes != codes_len) return UOR_SHORT_BUFFER;
+    if (ncodes != 0 && codes == nullptr) return UOR_SHORT_BUFFER;
+    Placed A, C;
+    int st;
+    if ((st = place(a, eb, &A))) return st;
+    if ((st = place(c, eb, &C))) return st;
+    const uint64_t k = transposed ? w_cols : w_rows, n = transposed ? w_rows : w_cols;
+    if (A.cols != k || C.rows != A.rows || C.cols != n) return UOR_NONCONFORMANT;
+    if (self_aliases(C.rows, C.cols, C.rs, C.cs)) return UOR_OUTPUT_ALIASES_ITSELF;
+    if (C.rows == 0 || C.cols == 0) return UOR_OK;
+    if ((((uintptr_t)table) & (uintptr_t)(eb - 1)) || (code_bits == 16 && ((uintptr_t)codes & 1)))
+        return UOR_INVALID_ARGUMENT;
+    // The decoded operand lives in the offer: there is no decode-free float
+    // route, so an offer below its size is refused before any launch.
+    const uint64_t wbytes = k ? round_up(k * n * (uint64_t)eb, 256) : 0;
+    const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+    const uint64_t have = scratch && scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
+    if (k > 0 && have < wbytes) return UOR_INVALID_ARGUMENT;
+    hipStream_t s = (hipStream_t)stream;
+    char *sc = (char *)p1;
+    if (k > 0) {
+        const dim3 grid((unsigned)((n + 255) / 256), (unsigned)(k < 65535 ? k : 65535));
+        if ((n + 255) / 256 > 0x7FFFFFFFull) return UOR_INVALID_ARGUMENT;
+        if (is_f64)
+            hipLaunchKernelGGL(arena_decode_kernel<double>, grid, dim3(256), 0, s, (const double *)table, entries,
+                               (const uint8_t *)codes, code_bits / 8, w_cols, transposed, k, n, (double *)sc);
+        else
+            hipLaunchKernelGGL(arena_decode_kernel<float>, grid, dim3(256), 0, s, (const float *)table, entries,
+                               (const uint8_t *)codes, code_bits / 8, w_cols, transposed, k, n, (float *)sc);
+        UOR_HIP(hipGetLastError());
+    }
+    const uor_view bv{k ? (void *)sc : (void *)sc, k * n, k, n, (int64_t)n, 1};
+    st = uor_gfx950_gemm_float(is_f64, a, &bv, c, alpha, beta, encode, sc + wbytes, have - wbytes, stream, route);
+    if (route && st == UOR_OK) route->launches += k > 0 ? 1 : 0;
+    return st;
+}

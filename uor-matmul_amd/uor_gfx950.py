@@ -43,6 +43,8 @@ SYMBOLS = [
     "uor_gfx950_suggested_scratch_coded",
     "uor_gfx950_gemm_coded_collapsed",
     "uor_gfx950_suggested_scratch_coded_collapse",
+    "uor_gfx950_gemm_coded_float",
+    "uor_gfx950_suggested_scratch_coded_float",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
     "uor_gfx950_sgemm",
@@ -146,6 +148,12 @@ def lib():
             L.uor_gfx950_gemm_coded_collapsed.restype = _i32
             L.uor_gfx950_suggested_scratch_coded_collapse.argtypes = [_u64, _u64, _u64]
             L.uor_gfx950_suggested_scratch_coded_collapse.restype = _u64
+            L.uor_gfx950_gemm_coded_float.argtypes = [_i32, _PV, _vp, _u64, _i32, _vp, _u64, _u64,
+                                                      _u64, _i32, _PV, _i64, _i64, _i32, _vp, _u64,
+                                                      _vp, _PR]
+            L.uor_gfx950_gemm_coded_float.restype = _i32
+            L.uor_gfx950_suggested_scratch_coded_float.argtypes = [_i32, _u64, _u64, _u64]
+            L.uor_gfx950_suggested_scratch_coded_float.restype = _u64
         if hasattr(L, "uor_gfx950_gemm_float"):
             L.uor_gfx950_gemm_float.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32, _vp, _u64,
                                                 _vp, _PR]
@@ -406,3 +414,26 @@ def suggested_scratch_collapse(m, k, n):
 
 def suggested_scratch_coded_collapse(m, k, n):
     return lib().uor_gfx950_suggested_scratch_coded_collapse(m, k, n)
+
+
+def gemm_coded_float(a, a_shape, a_strides, table, codes, w_rows, w_cols, transposed, c, c_shape,
+                     c_strides, alpha=1, beta=0, encode="nearest", scratch=None, stream=None):
+    """A float product with an Arena-coded operand: `table` is a float32 /
+    float64 device tensor (the codebook), `codes` uint8 or int16 (u16 codes)."""
+    import torch
+    is64 = int(a.dtype == torch.float64)
+    av = view(a, *a_shape, *a_strides)
+    cv = view(c, *c_shape, *c_strides)
+    bits = 8 if codes.element_size() == 1 else 16
+    r = Route()
+    st = lib().uor_gfx950_gemm_coded_float(
+        is64, ctypes.byref(av), _ptr(table), table.numel(), bits, _ptr(codes), codes.numel(),
+        w_rows, w_cols, int(bool(transposed)), ctypes.byref(cv), int(alpha), int(beta),
+        ENCODE[encode], _ptr(scratch),
+        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ctypes.byref(r))
+    return st, r.as_dict()
+
+
+def suggested_scratch_coded_float(is64, m, k, n):
+    return lib().uor_gfx950_suggested_scratch_coded_float(int(is64), m, k, n)
