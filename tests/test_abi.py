@@ -93,3 +93,23 @@ def test_coded_and_witness_validation_without_a_gpu():
     assert sel(_v(P, 24, 4, 6, 0, 1)) == 2     # witness aliases itself
     assert sel(_v(P, 20, 4, 6, 6, 1)) == 3     # witness buffer too short
     assert sel(_v(P, 24, 4, 6, 6, 1), mech=7) == 4
+
+
+def test_coded_float_validation_without_a_gpu():
+    """gemm_coded_float's refusals, all on the host (fake addresses)."""
+    import uor_gfx950 as u
+    lib = u.lib()
+    P = 0x1000
+    a, c = _v(P, 2 * 257, 2, 257, 257, 1), _v(P, 2 * 13, 2, 13, 13, 1)
+
+    def call(is64=0, bits=8, codes_len=13 * 257, w_rows=13, w_cols=257, entries=256, c=c, sc=0):
+        return lib.uor_gfx950_gemm_coded_float(is64, ctypes.byref(a), P, entries, bits, P, codes_len,
+                                               w_rows, w_cols, 1, ctypes.byref(c), 1, 0, 0,
+                                               P if sc else None, sc, None, None)
+    assert call(is64=2) == 4
+    assert call(bits=12) == 4
+    assert call(entries=0) == 4
+    assert call(codes_len=13 * 257 - 1) == 3                    # CodedMatrix::new
+    assert call(w_rows=14, codes_len=14 * 257) == 1             # C is 2 x 13
+    assert call(c=_v(P, 26, 2, 13, 0, 1)) == 2                  # aliasing C
+    assert call(sc=16) == 4                                     # offer below the decoded operand
