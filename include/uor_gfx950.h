@@ -219,6 +219,14 @@ uint64_t uor_gfx950_suggested_scratch_lut4(uint64_t m, uint64_t k, uint64_t n);
 #define UOR_TIER_BOOK 2     /* table[(code % entries) * block + i % block]  :268-309 */
 #define UOR_TIER_SIGN 3     /* bit i % block of the code: 1 -> +1, else -1  :362-401 */
 #define UOR_TIER_TERNARY 4  /* digit i % block: 0 -> -1, 2 -> +1, 1/3 -> 0  :466-517 */
+/* Tiers that only name a manifest here (TierId, tier.rs:265-278): the
+ * composing tiers of a uor_codec (Packed, Offset) and those with no GPU
+ * descriptor (Runs, Transcode) or a float one (Arena). */
+#define UOR_TIER_PACKED 5
+#define UOR_TIER_OFFSET 6
+#define UOR_TIER_RUNS 7
+#define UOR_TIER_TRANSCODE 8
+#define UOR_TIER_ARENA 9
 
 /*
  * A constructed codec (Codec<i8, Bd>, codecs.rs), as the GPU reads it:
@@ -390,6 +398,20 @@ int uor_gfx950_gemm_collapsed_i8(const uor_view *a, const uor_view *b, const uor
 /* The offer that lets gemm_collapsed_i8 collapse (suggested_collapse_index
  * plus suggested_collapse_rows, collapse.rs:103-120, and the product's). */
 uint64_t uor_gfx950_suggested_scratch_collapse(uint64_t m, uint64_t k, uint64_t n);
+
+/*
+ * Manifest::write_canonical_json (crates/uor-matmul-codec/src/kappa.rs:
+ * 321-360, CK-08): the canonical manifest of a coded artifact -- block,
+ * bound (a u128 as two halves), both digests, cols, rows, spec, tier, keys in
+ * that order -- into out[0..out_len).  *written gets the length (or, with
+ * UOR_SHORT_BUFFER, the length needed: BufferTooSmall).  A digest that is not
+ * `sha256:` + 64 lowercase hex, or an unknown tier, is UOR_INVALID_ARGUMENT
+ * (MalformedDigest).  Host code: no device, no stream.
+ */
+int uor_gfx950_manifest_json(int tier, uint64_t bound_lo, uint64_t bound_hi, uint64_t rows,
+                             uint64_t cols, uint64_t block, const char *codebook_sha256,
+                             const char *codes_sha256, const char *spec, char *out,
+                             uint64_t out_len, uint64_t *written);
 
 /* ================================================ (max, +) over Trop<i8> */
 

@@ -45,6 +45,7 @@ SYMBOLS = [
     "uor_gfx950_suggested_scratch_coded_collapse",
     "uor_gfx950_gemm_coded_float",
     "uor_gfx950_suggested_scratch_coded_float",
+    "uor_gfx950_manifest_json",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
     "uor_gfx950_sgemm",
@@ -70,7 +71,8 @@ class Codec(ctypes.Structure):
                 ("table_len", ctypes.c_uint64)]
 
 
-TIER = {"identity": 0, "grid": 1, "book": 2, "sign": 3, "ternary": 4}
+TIER = {"identity": 0, "grid": 1, "book": 2, "sign": 3, "ternary": 4, "packed": 5, "offset": 6,
+        "runs": 7, "transcode": 8, "arena": 9}
 
 
 class Route(ctypes.Structure):
@@ -154,6 +156,12 @@ def lib():
             L.uor_gfx950_gemm_coded_float.restype = _i32
             L.uor_gfx950_suggested_scratch_coded_float.argtypes = [_i32, _u64, _u64, _u64]
             L.uor_gfx950_suggested_scratch_coded_float.restype = _u64
+        if hasattr(L, "uor_gfx950_manifest_json"):
+            L.uor_gfx950_manifest_json.argtypes = [_i32, _u64, _u64, _u64, _u64, _u64,
+                                                   ctypes.c_char_p, ctypes.c_char_p,
+                                                   ctypes.c_char_p, ctypes.c_char_p, _u64,
+                                                   ctypes.POINTER(_u64)]
+            L.uor_gfx950_manifest_json.restype = _i32
         if hasattr(L, "uor_gfx950_gemm_float"):
             L.uor_gfx950_gemm_float.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32, _vp, _u64,
                                                 _vp, _PR]
@@ -437,3 +445,17 @@ def gemm_coded_float(a, a_shape, a_strides, table, codes, w_rows, w_cols, transp
 
 def suggested_scratch_coded_float(is64, m, k, n):
     return lib().uor_gfx950_suggested_scratch_coded_float(int(is64), m, k, n)
+
+
+def manifest_json(tier, bound, rows, cols, block, codebook_sha256, codes_sha256,
+                  spec="uor-matmul/1", out_len=512):
+    """Manifest::write_canonical_json: (status, text or the length needed)."""
+    buf = ctypes.create_string_buffer(max(out_len, 1))
+    n = _u64(0)
+    st = lib().uor_gfx950_manifest_json(
+        TIER.get(tier, tier), bound & ((1 << 64) - 1), bound >> 64, rows, cols, block,
+        codebook_sha256.encode(), codes_sha256.encode(), spec.encode(),
+        buf if out_len else None, out_len, ctypes.byref(n))
+    if st == 0:
+        return st, buf.raw[:n.value].decode()
+    return st, n.value
