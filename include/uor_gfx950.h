@@ -197,7 +197,8 @@ uint64_t uor_gfx950_suggested_scratch_int(int elem_bytes, uint64_t m, uint64_t k
  * a per-group codebook is ceil(n/group) reference calls over 128-row
  * CodedMatrix slices and MatViewMut column windows of C; group == n is one.
  * c: m x n view of `out_type` elements.  Epilogue and encode as gemm_i8.
- * For m >= 128, an offer of uor_gfx950_suggested_scratch_lut4 bytes decodes
+ * For m >= 128 (m >= 80 at k >= 4096), an offer of
+ * uor_gfx950_suggested_scratch_lut4 bytes decodes
  * W^T once into it and runs the dense int8 route (the reference's
  * decode-then-multiply spelling of the same value, coded.rs:98-140, CD-13);
  * any smaller offer, the table-lookup kernels.  The bytes are the same.

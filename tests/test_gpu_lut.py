@@ -171,10 +171,12 @@ def test_tiles_per_cu(uor, dev, m, k, n):
 
 @pytest.mark.parametrize("m,k,n,group,out,alpha,beta,code_offset", [
     (128, 2048, 96, 32, np.int32, 1, 0, 0), (200, 1000, 333, 7, np.int64, 3, -1, 0),
-    (130, 256, 45, 4, np.int16, 1 << 40, -(1 << 35), 3), (300, 130, 1000, 128, np.int8, 3, -1, 0)])
+    (130, 256, 45, 4, np.int16, 1 << 40, -(1 << 35), 3), (300, 130, 1000, 128, np.int8, 3, -1, 0),
+    (96, 4096, 300, 128, np.int32, 3, -1, 0), (80, 4352, 260, 32, np.int64, -2, 5, 0)])
 def test_prefill_decode_then_dense(oracle, uor, dev, m, k, n, group, out, alpha, beta, code_offset):
-    """m >= 128 with the suggested offer: W^T decoded once into the offer,
-    then the dense int8 route (ragged n, k not a multiple of the 32-weight
+    """m >= 128 (m >= 80 at k >= 4096) with the suggested offer: W^T decoded
+    once into the offer, then the dense int8 route (ragged n, k not a
+    multiple of the 32-weight
     decode chunk, unaligned code rows, every output width's epilogue).  The
     same bytes as the oracle; without the offer the table-lookup kernels."""
     route = run_case(oracle, uor, dev, m, k, n, group, seed=m + n, out=out, alpha=alpha, beta=beta,

@@ -776,7 +776,10 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
 
 // ------------------------------------------- many rows: decode, then dense
 //
-// For m >= LUT_PREFILL_M the weights are decoded once into W^T (k x n int8,
+// For m >= LUT_PREFILL_M (or m >= 80 at k >= 4096, where the dense route
+// takes its 256-wide tile: m = 80..112 at the config weights 0.18 ms against
+// 0.20-0.26 ms for the table-lookup kernel) the weights are decoded once into
+// W^T (k x n int8,
 // row-major, leading dimension ldw, a multiple of 16) and the product runs on
 // the dense int8 MFMA route: the reference's decode-then-multiply spelling of
 // the same value (coded_gemm, crates/uor-matmul-gemm/src/coded.rs:98-140;
@@ -785,6 +788,8 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
 // 128 and 64 of the weights), then writes the tile's 128 rows of W^T as
 // 128-byte row segments (8 lanes x 16 bytes per row).
 constexpr uint64_t LUT_PREFILL_M = 128;
+
+static bool lut_prefill(uint64_t m, uint64_t k) { return m >= LUT_PREFILL_M || (m >= 80 && k >= 4096); }
 
 __global__ void __launch_bounds__(256) lut4_decode_t_kernel(LutArgs L, int book_aligned, int code_fast,
                                                             int8_t *wt, uint64_t ldw) {
@@ -872,10 +877,10 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         route->operand_modes = fast;
     }
     const bool a16 = A.cs == 1 && ((uintptr_t)A.base % 16 == 0) && (A.rs % 16 == 0 || m == 1);
-    // m >= LUT_PREFILL_M with an offer that holds W^T: decode, then the dense
+    // lut_prefill(m, k) with an offer that holds W^T: decode, then the dense
     // int8 route (whatever is left of the offer goes to it).
     const uint64_t ldw = (n + 15) / 16 * 16;
-    if (m >= LUT_PREFILL_M && scratch && k > 0 && k <= (1ull << 40) / ldw) {
+    if (lut_prefill(m, k) && scratch && k > 0 && k <= (1ull << 40) / ldw) {
         const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
         const uint64_t have = scratch_bytes > (p1 - p0) ? scratch_bytes - (p1 - p0) : 0;
         const uint64_t wbytes = (k * ldw + 255) & ~255ull;
@@ -984,9 +989,9 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
 }
 
 extern "C" uint64_t uor_gfx950_suggested_scratch_lut4(uint64_t m, uint64_t k, uint64_t n) {
-    // W^T for the decode-then-dense route (m >= LUT_PREFILL_M), plus the
+    // W^T for the decode-then-dense route (lut_prefill(m, k)), plus the
     // dense route's own offer; none below (the LUT kernels use no scratch).
-    if (m < LUT_PREFILL_M || k == 0 || n == 0) return 0;
+    if (!lut_prefill(m, k) || k == 0 || n == 0) return 0;
     const uint64_t ldw = (n + 15) / 16 * 16;
     return 256 + ((k * ldw + 255) & ~255ull) + uor_gfx950_suggested_scratch_i8(m, k, n);
 }
