@@ -47,6 +47,17 @@ SPECS = {
 }
 
 
+def code_bytes(spec):
+    return 1 if spec.get("packed") or spec.get("code_bits", 16) == 8 else 2
+
+
+def table_variant(spec, m, k):
+    """The few-rows code-table kernel's conditions at a row-major A of depth k."""
+    mb, cb = max_block(spec), code_bytes(spec)
+    win = k % 16 == 0 and (k // mb) * cb % 16 == 0 and (16 // cb) * mb % 16 == 0
+    return win and cb == 1 and ((mb in (4, 8) and m <= 4) or (mb == 4 and m <= 8))
+
+
 def max_block(spec):
     ib = spec.get("block", 1) if spec["tier"] in ("book", "sign", "ternary") else 1
     return (spec.get("packed") or 1) * ib
@@ -99,8 +110,10 @@ def test_tiers_against_oracle(oracle, uor, dev, name, transposed, offer, m):
     st, route = run(oracle, uor, dev, SPECS[name], m, k, n, transposed, offer, alpha=3, beta=-2,
                     seed=len(name) + m)
     assert st == "ok"
-    want = ("coded_gemv" if transposed and m <= 8 else
-            "coded_dense" if offer else "coded_direct")
+    # Past four rows the register route keeps only the code-table variant
+    # when the offer would hold the decode-into-scratch route.
+    few = transposed and m <= 8 and (m <= 4 or table_variant(SPECS[name], m, k) or not offer)
+    want = "coded_gemv" if few else "coded_dense" if offer else "coded_direct"
     assert route["kind"] == want, route
 
 
@@ -136,7 +149,7 @@ def test_few_rows_code_windows(oracle, uor, dev, name, m):
         assert st == "ok" and route["kind"] == "coded_gemv", route
         a_vec = k % 16 == 0
         win = a_vec and (16 // cb) * mb % 16 == 0
-        lut = win and cb == 1 and mb in (4, 8) and m <= 4
+        lut = table_variant(spec, m, k)
         assert route["operand_modes"] == (3 if lut else 2 if win else 1 if a_vec else 0), route
 
 

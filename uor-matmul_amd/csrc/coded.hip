@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(256) coded_gemv_win_kernel(CodedArgs W, GemvAr
 // code costs one byte extract, D LDS reads and D x MR v_dot4_i32_i8.  A wave
 // takes 4 columns: the A bytes of a window are loaded once for all four, and
 // each column's next code window is loaded before this one is used.
-template <int MR, int D>
+template <int MR, int D, int NCOL = 4>
 __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvArgs G) {
     __shared__ uint32_t lut[256 * D];
     for (int idx = threadIdx.x; idx < 256 * D; idx += 256) {
@@ -462,25 +462,25 @@ __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvAr
     }
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const uint64_t jb = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    const uint64_t jb = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * NCOL;
     if (jb >= G.n) return;  // whole waves, after the barrier
     const uint64_t nwin = W.per_row / 16;  // one-byte codes: a row is per_row bytes
     constexpr int E = 64 * D;              // elements per 16-byte window
-    int acc[4][MR];
+    int acc[NCOL][MR];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NCOL; ++c)
 #pragma unroll
         for (int r = 0; r < MR; ++r) acc[c][r] = 0;
-    uint4 nxt[4];
+    uint4 nxt[NCOL];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NCOL; ++c)
         nxt[c] = ((uint64_t)lane < nwin && jb + c < G.n)
                      ? *(const uint4 *)(W.codes + (jb + c) * W.per_row + 16 * (uint64_t)lane)
                      : uint4{0, 0, 0, 0};
     for (uint64_t wi = (uint64_t)lane; wi < nwin; wi += 64) {
-        uint4 cur[4];
+        uint4 cur[NCOL];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < NCOL; ++c) {
             cur[c] = nxt[c];
             if (wi + 64 < nwin && jb + c < G.n)
                 nxt[c] = *(const uint4 *)(W.codes + (jb + c) * W.per_row + 16 * (wi + 64));
@@ -498,7 +498,7 @@ __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvAr
                 a[r][4 * h + 3] = v.w;
             }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < NCOL; ++c) {
             const uint32_t d[4] = {cur[c].x, cur[c].y, cur[c].z, cur[c].w};
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
@@ -514,7 +514,7 @@ __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvAr
         }
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NCOL; ++c)
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             int64_t v = acc[c][r];
@@ -527,9 +527,16 @@ __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvAr
 
 template <int MR>
 static void launch_gemv_lut(const CodedArgs &W, const GemvArgs &G, hipStream_t s) {
-    const dim3 grid((unsigned)((G.n + 15) / 16));
-    if (W.cd.mb == 4) hipLaunchKernelGGL((coded_gemv_lut_kernel<MR, 1>), grid, dim3(256), 0, s, W, G);
-    else hipLaunchKernelGGL((coded_gemv_lut_kernel<MR, 2>), grid, dim3(256), 0, s, W, G);
+    if constexpr (MR == 8) {
+        // Eight rows: two columns per wave, four-element codes only (the
+        // eight-element codes' A window would not fit beside them).
+        const dim3 grid((unsigned)((G.n + 7) / 8));
+        hipLaunchKernelGGL((coded_gemv_lut_kernel<8, 1, 2>), grid, dim3(256), 0, s, W, G);
+    } else {
+        const dim3 grid((unsigned)((G.n + 15) / 16));
+        if (W.cd.mb == 4) hipLaunchKernelGGL((coded_gemv_lut_kernel<MR, 1>), grid, dim3(256), 0, s, W, G);
+        else hipLaunchKernelGGL((coded_gemv_lut_kernel<MR, 2>), grid, dim3(256), 0, s, W, G);
+    }
 }
 
 template <int TIER, int MR>
@@ -740,6 +747,10 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
         }
     }
 
+    const uint64_t wbytes = k ? decoded_bytes(k, n) : 0;
+    const bool dense = k > 0 && scratch && scratch_bytes >= wbytes + uor_gfx950_suggested_scratch_i8(m, k, n) &&
+                       (n + 127) / 128 <= 0x7FFFFFFFull && (k + 127) / 128 <= 65535ull &&
+                       (k * (round_up(n, 16) / 16) + 255) / 256 <= 0x7FFFFFFFull;
     if (transposed && k > 0 && m <= 8 && k <= GEMV_MAX_K && (n + 3) / 4 <= 0x7FFFFFFFull) {
         const bool a_vec = A.cs == 1 && A.rs > 0 && (A.rs % 16) == 0 && ((uintptr_t)A.base & 15) == 0;
         GemvArgs G{(const int8_t *)A.base, A.rs, A.cs, a_vec ? 1 : 0, C.base, C.rs, C.cs, m, k, n,
@@ -749,9 +760,16 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
         const uint64_t row_bytes = W.per_row * (uint64_t)W.cb;
         const bool win = a_vec && row_bytes % 16 == 0 && ((uintptr_t)codes & 15) == 0 &&
                          ((16 / (uint64_t)W.cb) * W.cd.mb) % 16 == 0;
-        // The table variant: one-byte codes of 4 or 8 elements, m <= 4.
-        const bool lut = win && W.cb == 1 && (W.cd.mb == 4 || W.cd.mb == 8) && m <= 4 &&
+        // The table variant: one-byte codes of 4 or 8 elements, m <= 4; of 4
+        // elements, m <= 8.
+        const bool lut = win && W.cb == 1 &&
+                         (((W.cd.mb == 4 || W.cd.mb == 8) && m <= 4) || (W.cd.mb == 4 && m <= 8)) &&
                          (n + 15) / 16 <= 0x7FFFFFFFull;
+        // Past four rows the per-element decode costs more than decoding
+        // into the scratch (Ternary<4,u8> at the config weights, m = 5: 244
+        // against about 180 us): with the offer, the dense route below.
+        const bool gemv = m <= 4 || lut || !dense;
+        if (gemv) {
         if (route) {
             route->kind = UOR_ROUTE_CODED_GEMV;
             route->tile_m = (int)m;
@@ -764,17 +782,15 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
         if (lut) {
             if (m <= 1) launch_gemv_lut<1>(W, G, s);
             else if (m <= 2) launch_gemv_lut<2>(W, G, s);
-            else launch_gemv_lut<4>(W, G, s);
+            else if (m <= 4) launch_gemv_lut<4>(W, G, s);
+            else launch_gemv_lut<8>(W, G, s);
         } else {
             launch_gemv(W, G, win, s);
         }
         UOR_HIP(hipGetLastError());
         return UOR_OK;
+        }
     }
-    const uint64_t wbytes = k ? decoded_bytes(k, n) : 0;
-    const bool dense = k > 0 && scratch && scratch_bytes >= wbytes + uor_gfx950_suggested_scratch_i8(m, k, n) &&
-                       (n + 127) / 128 <= 0x7FFFFFFFull && (k + 127) / 128 <= 65535ull &&
-                       (k * (round_up(n, 16) / 16) + 255) / 256 <= 0x7FFFFFFFull;
     if (dense) {
         const uint64_t ldw = round_up(n, 16);
         int8_t *wt = (int8_t *)scratch;
