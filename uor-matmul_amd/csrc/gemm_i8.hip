@@ -1259,10 +1259,11 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
     // m = 128 in 0.080 ms, where the 128-wide tile took 0.337, 0.155 and
     // 0.136 ms (1024 x 4096 x 4096: 0.047 against 0.074 ms).  At 16 tiles the
     // two are even (512 x 2048 x 2048: 0.030 against 0.026 ms), hence 32.
-    // From 64 rows up it still wins at depth (64 x 8192 x 28672: 0.091
-    // against 0.137 ms) but not at k = 2048 (100 x 2048 x 16384: 0.039
+    // From 16 rows up it still wins at depth (64 x 8192 x 28672: 0.091
+    // against 0.137 ms; 16 rows 0.088 against 0.128 ms; 24 x 16384 x 16384
+    // 0.129 against 0.200 ms) but not at k = 2048 (100 x 2048 x 16384: 0.039
     // against 0.032 ms).
-    const bool use256 = t256 >= 256 || (N >= 128 && t256 >= 32 && (M >= 128 || (M >= 64 && K >= 4096)));
+    const bool use256 = t256 >= 256 || (N >= 128 && t256 >= 32 && (M >= 128 || (M >= 16 && K >= 4096)));
     int bm;
     if (use256 && dl_ok(pair, K, N)) {
         bm = 256;
