@@ -405,11 +405,13 @@ def test_splitk_narrow_tile_folds_segments(uor, dev):
     assert np.array_equal(c.cpu().numpy().reshape(m, n), S)
 
 
-@pytest.mark.parametrize("m,k,n", [(512, 1024, 28672), (256, 2048, 28672), (300, 640, 20000)])
+@pytest.mark.parametrize("m,k,n", [(512, 1024, 28672), (256, 2048, 28672), (300, 640, 20000),
+                                   (16, 4096, 8192), (40, 4160, 8208), (100, 4096, 9008)])
 @pytest.mark.parametrize("out", ["i32", "i64"])
 def test_wide_tile_below_one_round(uor, dev, m, k, n, out):
-    """Fewer 256-wide tiles than CUs, wide n: the 256-wide tile (one round)
-    rather than several rounds of 128-wide tiles; ragged edges included.
+    """Fewer 256-wide tiles than CUs, wide n (and from 16 rows at k >= 4096):
+    the 256-wide tile (one round) rather than several rounds of narrower
+    tiles; ragged edges included (rows past m read the last row).
     Checked in float64 on the device (|3 AB - C| < 2^53)."""
     g = torch.Generator(device=dev).manual_seed(m + n)
     a = torch.randint(-128, 128, (m * k,), dtype=torch.int8, device=dev, generator=g)
