@@ -50,10 +50,13 @@ def log(msg):
 SETTLE_S = 0.3  # untimed running before each timed region, so clocks reach steady state
 
 
-def settle(torch, step, seconds=SETTLE_S):
+def settle(torch, step, seconds=None):
     """Run `step` untimed for at least `seconds` of wall time (MI355X raises
     its shader clock over the first ~0.2 s of sustained load; a timed region
-    that starts cold measures the ramp, not the kernel)."""
+    that starts cold measures the ramp, not the kernel).  --settle sets the
+    default (0 under a profiler, where every dispatch is recorded)."""
+    if seconds is None:
+        seconds = SETTLE_S
     t0 = time.perf_counter()
     n = 0
     while time.perf_counter() - t0 < seconds:
@@ -639,6 +642,127 @@ def bench_int(args, torch, uor):
     return out
 
 
+def measured_peaks(torch):
+    """Calibration probes (uor-matmul_amd/probe/peaks.hip, libuor_probe.so):
+    the best HBM read rate of a plain grid-stride streaming kernel over three
+    rotating 128 MiB buffers (384 MiB, beyond the 256 MB Infinity Cache), and
+    the int8 MFMA rate of a 32x32x32 loop, one workgroup of four waves per
+    CU, on random and on constant operands, with the shader clock the loop
+    ran at (s_memtime ticks over s_memrealtime ticks times the wall-clock
+    rate).  These are what the kernels can reach on this box; the roofline
+    fractions are also reported against them."""
+    import ctypes
+    path = ROOT / "uor-matmul_amd" / "libuor_probe.so"
+    if not path.exists():
+        return None
+    P = ctypes.CDLL(str(path))
+    P.uor_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_void_p, ctypes.c_void_p]
+    P.uor_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.POINTER(ctypes.c_int)]
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nbytes = 128 << 20
+    bufs = [torch.full((nbytes,), r + 1, dtype=torch.uint8, device=dev) for r in range(3)]
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    reads = []
+    for bpc in (2, 4):
+        for variant in range(4):
+            def step(i):
+                st = P.uor_probe_read(bufs[i % 3].data_ptr(), nbytes, bpc * cus, variant,
+                                      sink.data_ptr(), stream.cuda_stream)
+                if st != 0:
+                    raise RuntimeError(f"probe read status {st}")
+            for i in range(6):
+                step(i)
+            torch.cuda.synchronize()
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record(stream)
+            for i in range(60):
+                step(i)
+            s1.record(stream)
+            torch.cuda.synchronize()
+            us = s0.elapsed_time(s1) / 60 * 1e3
+            reads.append({"blocks_per_cu": bpc, "unroll": 8 if variant & 2 else 4,
+                          "nontemporal": bool(variant & 1), "us": round(us, 3),
+                          "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    best = max(reads, key=lambda r: r["GB_s"])
+    del bufs
+    out = {"hbm_read_GB_s": best["GB_s"], "hbm_read_best": best,
+           "hbm_read_runs": reads}
+    iters = 3000
+    blocks = cus
+    ops_n = blocks * 256 * 16 * 4
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    for name, ops in (("random", torch.randint(-2 ** 31, 2 ** 31 - 1, (ops_n,), dtype=torch.int32,
+                                               device=dev)),
+                      ("constant", torch.full((ops_n,), 0x01010101, dtype=torch.int32, device=dev))):
+        wall = ctypes.c_int(0)
+
+        def run():
+            st = P.uor_probe_mfma(ops.data_ptr(), blocks, iters, 4, clk.data_ptr(), sink.data_ptr(),
+                                  stream.cuda_stream, ctypes.byref(wall))
+            if st != 0:
+                raise RuntimeError(f"probe mfma status {st}")
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.3:  # the same settling as the kernels get
+            run()
+            torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(5):
+            run()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / 5
+        ops_done = blocks * 4 * iters * 32 * 65536.0
+        c = clk.view(blocks, 2).cpu().double()
+        mhz = float((c[:, 0] / c[:, 1]).mean() * wall.value / 1e3) if wall.value else None
+        out[f"mfma_i8_{name}_TOPS"] = round(ops_done / (ms * 1e-3) / 1e12, 1)
+        out[f"mfma_i8_{name}_clock_MHz"] = round(mhz, 1) if mhz else None
+    return out
+
+
+def bench_config1(args, torch, uor, gen):
+    """configs[0]: slice::gemm i8 x i8 -> i32 at m = k = n = 1024, row-major,
+    the reference's own xorshift operands (salts 1, 2), the suggested scratch
+    offer; launch-bound at this size.  Checked in float64 (exact here)."""
+    n = 1024
+    dev = torch.device("cuda:0")
+    a = gen.i8_full(n * n, 1, exact_sequence=True)
+    b = gen.i8_full(n * n, 2, exact_sequence=True)
+    ga, gb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    gc = torch.zeros(n * n, dtype=torch.int32, device=dev)
+    sc = torch.empty(uor.suggested_scratch_i8(n, n, n), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        st = uor.slice_gemm_i8(n, n, n, ga, gb, gc, scratch=sc, stream=stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"slice::gemm status {st}")
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    settle(torch, step)
+    steps = max(50, args.steps)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(steps):
+        step()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    ms = s0.elapsed_time(s1) / steps
+    A = ga.view(n, n).to(torch.float64)
+    B = gb.view(n, n).to(torch.float64)
+    parity = bool(torch.equal(gc.view(n, n).to(torch.float64), A @ B))
+    return {"config": "BASELINE configs[0]: slice::gemm i8 -> i32, 1024^3, xorshift operands, "
+                      "suggested offer", "m": n, "k": n, "n": n, "ms_per_call": round(ms, 5),
+            "TOPS": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1), "parity": parity}
+
+
 def cpu_baseline_i8(host, oracle):
     """The reference's packed route restated (oracle/fastroute.cpp) on a row
     slab of the same 8192^3 problem, all usable host cores."""
@@ -675,7 +799,12 @@ def cpu_baseline_i8(host, oracle):
     }
 
 
+PARTS = ["i8", "config1", "deep", "lut", "prefill", "coded", "collapse", "trop", "float", "int",
+         "peaks", "cpu"]
+
+
 def main():
+    global SETTLE_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -685,6 +814,12 @@ def main():
     ap.add_argument("--no-trop", action="store_true", help="skip the secondary max-plus figure")
     ap.add_argument("--no-float", action="store_true", help="skip the secondary exact-float figure")
     ap.add_argument("--no-int", action="store_true", help="skip the i16/i32/i64 element figure")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated parts to run (" + ",".join(PARTS) + "), e.g. for a "
+                         "profiler run of one kernel family; the line then holds only those")
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="seconds of untimed running before each timed region (0 under a profiler)")
+    ap.add_argument("--lut-m", default="1,8,32", help="LUT decode row counts")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device-to-device copy and exit (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -693,6 +828,24 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(sharding is design-only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    SETTLE_S = max(0.0, args.settle)
+    if args.only:
+        parts = set(x.strip() for x in args.only.split(",") if x.strip())
+        unknown = parts - set(PARTS)
+        if unknown:
+            ap.error(f"unknown parts {sorted(unknown)}")
+    else:
+        parts = set(PARTS)
+        if args.no_lut:
+            parts -= {"lut", "prefill", "coded", "collapse"}
+        if args.no_trop:
+            parts.discard("trop")
+        if args.no_float:
+            parts.discard("float")
+        if args.no_int:
+            parts.discard("int")
+        if args.no_cpu_baseline:
+            parts.discard("cpu")
     import torch
     if args.copy_calibration:
         n = 1 << 30
@@ -706,50 +859,72 @@ def main():
     import uor_gfx950 as uor
     import gen
     uor.lib()
-    result, host = bench_i8(args, torch, uor, gen)
-    log("[bench] deep reduction")
-    result["deep"] = {
-        "metric": "deep exact i8 GEMM GB/s (% HBM peak)",
-        "config": "BASELINE configs[1] deep case: m=n=128, k=2^24, A=B=-128, i64 out",
-        "run": bench_deep(args, torch, uor),
-    }
-    if not args.no_lut:
+    result, host = {"metric": METRIC, "parts": sorted(parts)}, None
+    if "i8" in parts:
+        result, host = bench_i8(args, torch, uor, gen)
+    if "config1" in parts:
+        log("[bench] config 1 (1024^3 slice::gemm)")
+        result["config1"] = bench_config1(args, torch, uor, gen)
+    if "deep" in parts:
+        log("[bench] deep reduction")
+        result["deep"] = {
+            "metric": "deep exact i8 GEMM GB/s (% HBM peak)",
+            "config": "BASELINE configs[1] deep case: m=n=128, k=2^24, A=B=-128, i64 out",
+            "run": bench_deep(args, torch, uor),
+        }
+    if "lut" in parts:
         log("[bench] lut4 decode")
-        lut = bench_lut4(args, torch, uor, gen)
+        ms_list = tuple(int(x) for x in args.lut_m.split(",") if x)
         result["secondary"] = {
             "metric": "LUT-GEMM decode GB/s (% HBM peak)",
             "unit": "GB/s",
             "peak": PEAK_HBM_GBS,
             "config": "BASELINE configs[2]: 4-bit codes, k=8192, n=28672, group=128, "
                       "3 rotating code buffers (>256 MB MALL)",
-            "runs": lut,
-            "prefill": bench_lut_prefill(args, torch, uor, gen),
-            "ternary": bench_coded(args, torch, uor, gen),
+            "runs": bench_lut4(args, torch, uor, gen, ms_list),
         }
+    if "prefill" in parts:
+        log("[bench] lut4 prefill")
+        result.setdefault("secondary", {})["prefill"] = bench_lut_prefill(args, torch, uor, gen)
+    if "coded" in parts:
+        log("[bench] coded operands")
+        result.setdefault("secondary", {})["ternary"] = bench_coded(args, torch, uor, gen)
+    if "collapse" in parts:
         log("[bench] collapse")
         result["collapse"] = bench_collapse(args, torch, uor, gen)
-    if not args.no_trop:
+    if "trop" in parts:
         log("[bench] trop max-plus")
         result["tropical"] = {
             "metric": "Trop<i8> max-plus terms/s (% packed-i16 VALU peak)",
             "config": "BASELINE configs[4]: m=n=k=4096, 5% -inf entries, Trop<i32> output",
             "run": bench_trop(args, torch, uor, gen),
         }
-    if not args.no_float:
+    if "float" in parts:
         log("[bench] exact float")
         result["float"] = {
             "metric": "exact float GEMM TFLOP/s (2mnk per second, rounded once)",
             "config": "BASELINE configs[3]",
             "runs": bench_float(args, torch, uor, gen),
         }
-    if not args.no_int:
+    if "int" in parts:
         log("[bench] i16/i32/i64 elements")
         result["integer"] = {
             "metric": "exact integer GEMM TOPS (2mnk per second), i16/i32/i64 elements",
             "config": "the Kernelized i16/i32/i64 families, full-range operands",
             "runs": bench_int(args, torch, uor),
         }
-    if not args.no_cpu_baseline:
+    if "peaks" in parts:
+        log("[bench] measured peaks")
+        peaks = measured_peaks(torch)
+        if peaks:
+            result["measured_peaks"] = peaks
+            if "roofline" in result and peaks.get("mfma_i8_random_TOPS"):
+                rf = result["roofline"]
+                rf["measured_peak"] = peaks["mfma_i8_random_TOPS"]
+                rf["frac_measured_peak"] = round(rf["achieved"] / peaks["mfma_i8_random_TOPS"], 4)
+            for r in result.get("secondary", {}).get("runs", []):
+                r["frac_measured_read_peak"] = round(r["GB_s"] / peaks["hbm_read_GB_s"], 4)
+    if "cpu" in parts and host is not None:
         from oracle import oracle
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline_i8(host, oracle)

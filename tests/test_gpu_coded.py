@@ -64,7 +64,7 @@ def max_block(spec):
 
 
 def run(oracle, uor, dev, spec, m, k, n, transposed, offer, out="i32", alpha=1, beta=0,
-        encode="nearest", seed=0, codes_len_delta=0, c_strides=None):
+        encode="nearest", seed=0, codes_len_delta=0, c_strides=None, offer_shift=0):
     rng = np.random.default_rng(seed)
     rows, cols = (n, k) if transposed else (k, n)
     mb = max_block(spec)
@@ -89,7 +89,8 @@ def run(oracle, uor, dev, spec, m, k, n, transposed, offer, out="i32", alpha=1, 
     scratch = None
     if offer:
         nb = uor.suggested_scratch_coded(m, k, n)
-        scratch = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
+        # offer_shift: a sub-buffer that starts off any aligned boundary.
+        scratch = torch.empty(nb + offer_shift, dtype=torch.uint8, device=dev)[offer_shift:] if nb else None
     gst, route = uor.gemm_coded(torch.from_numpy(a).to(dev), (m, k), (k, 1), gcd, gcodes, rows,
                                 cols, transposed, gc, (m, n), cs, out=out, alpha=alpha,
                                 beta=beta, encode=encode, scratch=scratch)
@@ -184,6 +185,17 @@ def test_larger_shapes_dense_route(oracle, uor, dev, name, transposed):
     and a dense route of several tiles."""
     m, k, n = 130, 432, 288
     st, route = run(oracle, uor, dev, SPECS[name], m, k, n, transposed, True, seed=7)
+    assert st == "ok" and route["kind"] == "coded_dense", route
+
+
+@pytest.mark.parametrize("shift", [1, 4, 12])
+@pytest.mark.parametrize("transposed", [True, False])
+def test_dense_route_unaligned_offer(oracle, uor, dev, shift, transposed):
+    """The decoded operand (16-byte stores) and the dense route's offer are
+    carved from the offer's first aligned byte, so a suggested offer that
+    starts anywhere still takes the dense route, with the oracle's bytes."""
+    st, route = run(oracle, uor, dev, SPECS["ternary4_u8"], 130, 256, 200, transposed, True,
+                    alpha=3, beta=-2, seed=shift, offer_shift=shift)
     assert st == "ok" and route["kind"] == "coded_dense", route
 
 

@@ -287,3 +287,51 @@ def test_crt_plan_is_tight(oracle, uor, dev):
     oracle.gemm_float(a.reshape(-1).copy(), (m, k), (k, 1), b.reshape(-1).copy(), (k, n), (n, 1),
                       want, (m, n), (n, 1))
     assert np.array_equal(bits(c.cpu().numpy()), bits(want))
+
+
+@pytest.mark.parametrize("is64,N", [(False, 4096), (True, 2048)])
+def test_config4_full_size_rows_and_columns(oracle, uor, dev, is64, N):
+    """configs[3] at its full size: f32 4096^3 (e in [-40, 40]) and f64 2048^3
+    (e in [-300, 300]), 1% zeros, 1% cancelling pairs, on the CRT route with
+    the suggested offer (the full-size grid, modulus batching and finish
+    choice).  Whole output rows and columns -- the first, the last and
+    seeded others -- are compared bit for bit with the oracle (ora_gemm_float,
+    the Complete-register restatement), and every cell with the direct route
+    where that is cheap (f32: rows are independent, so the direct route runs
+    on a 64-row slab)."""
+    a = gen.float_config4(N, N, is64, 9)
+    b = gen.float_config4(N, N, is64, 10)
+    a, b = gen.cancel_pairs(a, b, 99)
+    ft = np.float64 if is64 else np.float32
+    ga = torch.from_numpy(a.reshape(-1).copy()).to(dev)
+    gb = torch.from_numpy(b.reshape(-1).copy()).to(dev)
+    sc = offer_for(uor, dev, "full", is64, N, N, N)
+    gc = torch.full((N * N,), float("nan"), dtype=torch.float64 if is64 else torch.float32,
+                    device=dev)
+    st, route = uor.gemm_float(ga, (N, N), (N, 1), gb, (N, N), (N, 1), gc, (N, N), (N, 1),
+                               scratch=sc)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "float_crt", route
+    got = gc.cpu().numpy().reshape(N, N)
+    del sc
+    torch.cuda.empty_cache()
+    rng = np.random.default_rng(4 + is64)
+    rows = sorted({0, 1, N // 2, N - 1, *(int(x) for x in rng.integers(0, N, 4))})
+    cols = sorted({0, N - 1, *(int(x) for x in rng.integers(0, N, 2))})
+    bflat = b.reshape(-1).copy()
+    for i in rows:
+        want = np.zeros(N, ft)
+        assert oracle.gemm_float(a[i].copy(), (1, N), (N, 1), bflat, (N, N), (N, 1), want,
+                                 (1, N), (N, 1)) == "ok"
+        bad = np.nonzero(bits(got[i].copy()) != bits(want))[0]
+        assert bad.size == 0, f"row {i}: columns {bad[:5].tolist()}"
+    aflat = a.reshape(-1).copy()
+    for j in cols:
+        want = np.zeros(N, ft)
+        assert oracle.gemm_float(aflat, (N, N), (N, 1), b[:, j].copy(), (N, 1), (1, 1), want,
+                                 (N, 1), (1, 1)) == "ok"
+        bad = np.nonzero(bits(got[:, j].copy()) != bits(want))[0]
+        assert bad.size == 0, f"column {j}: rows {bad[:5].tolist()}"
+    # The cancelling pairs and exact zeros reach the checked cells: the rows
+    # hold exact zeros of the inputs.
+    assert (a[rows] == 0).any()

@@ -5,6 +5,8 @@ Bar: bit-exact.  Small and ragged cases compare with the CPU oracle
 matmul, which is exact here because every partial sum is an integer below
 2^53, plus oracle rows and closed forms for the deep case.
 """
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -77,7 +79,7 @@ def test_layouts_against_oracle(oracle, uor, dev, shape, layout):
 @pytest.mark.parametrize("encode", ["nearest", "saturating", "toward_zero", "wrapping"])
 def test_output_types_and_encodes(oracle, uor, dev, out, encode):
     dt = {"i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64}[out]
-    rng = np.random.default_rng(hash((out, encode)) & 0xFFFF)
+    rng = np.random.default_rng(zlib.crc32(f"{out}-{encode}".encode()))
     m, k, n = 37, 300, 41
     a = rng.integers(-128, 128, m * k).astype(np.int8)
     b = rng.integers(-128, 128, k * n).astype(np.int8)
@@ -191,6 +193,33 @@ def test_offer_ladder_same_bytes_cd10(oracle, uor, dev):
         assert np.array_equal(gc.cpu().numpy().reshape(m, n), want), route
         kinds.add(route["kind"])
     assert kinds == {"mfma_wide", "mfma_splitk"}
+
+
+@pytest.mark.parametrize("shift", [1, 4, 8, 12])
+def test_unaligned_offer_same_bytes(uor, dev, shift):
+    """An offer that starts off a 256-byte boundary (a sub-buffer) still
+    takes the split-K route, its i64 partial sums carved from the first
+    aligned byte, and gives the no-offer bytes."""
+    rng = np.random.default_rng(4100 + shift)
+    m, k, n = 72, 70_000, 40
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    ga, gb = to_dev(a, dev), to_dev(b, dev)
+    base = torch.empty(uor.suggested_scratch_i8(m, k, n) + shift, dtype=torch.uint8, device=dev)
+    offer = base[shift:]
+    assert offer.data_ptr() % 8 != 0 or shift % 8 == 0
+    outs = []
+    for scratch in (None, offer):
+        gc = torch.full((m * n,), 5, dtype=torch.int64, device=dev)
+        st, route = uor.gemm_i8(ga, (m, k), (k, 1), gb, (k, n), (n, 1), gc, (m, n), (n, 1),
+                                out="i64", alpha=-3, beta=2, scratch=scratch)
+        torch.cuda.synchronize()
+        assert st == 0
+        outs.append((gc.cpu().numpy(), route["kind"]))
+    assert outs[1][1] == "mfma_splitk" and outs[0][1] == "mfma_wide"
+    assert np.array_equal(outs[0][0], outs[1][0])
+    want = a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64)
+    assert np.array_equal(outs[0][0].reshape(m, n), (-3 * want + 10).astype(np.int64))
 
 
 def test_config1_slice_gemm_1024(uor, dev):

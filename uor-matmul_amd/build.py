@@ -48,7 +48,24 @@ def main() -> pathlib.Path:
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs),
                     "-o", str(tmp)], check=True)
     os.replace(tmp, OUT)
+    build_probe()
     return OUT
+
+
+PROBE_SRC = HERE / "probe" / "peaks.hip"
+PROBE_OUT = HERE / "libuor_probe.so"
+
+
+def build_probe() -> pathlib.Path:
+    """The calibration probes bench.py runs beside the library (measured HBM
+    read and int8 MFMA peaks); a library of their own."""
+    tmp = PROBE_OUT.with_suffix(".so.tmp")
+    r = subprocess.run([HIPCC, *FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {PROBE_SRC.name}:\n{r.stderr}")
+    os.replace(tmp, PROBE_OUT)
+    return PROBE_OUT
 
 
 if __name__ == "__main__":

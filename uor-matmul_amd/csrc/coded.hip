@@ -649,7 +649,7 @@ using namespace uor;
 
 extern "C" uint64_t uor_gfx950_suggested_scratch_coded(uint64_t m, uint64_t k, uint64_t n) {
     if (m == 0 || n == 0 || k == 0) return 0;
-    return decoded_bytes(k, n) + uor_gfx950_suggested_scratch_i8(m, k, n);
+    return 256 + decoded_bytes(k, n) + uor_gfx950_suggested_scratch_i8(m, k, n);
 }
 
 static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void *codes, uint64_t codes_len,
@@ -748,7 +748,11 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
     }
 
     const uint64_t wbytes = k ? decoded_bytes(k, n) : 0;
-    const bool dense = k > 0 && scratch && scratch_bytes >= wbytes + uor_gfx950_suggested_scratch_i8(m, k, n) &&
+    // The decoded operand takes 16-byte stores: the offer from its first
+    // aligned byte.
+    uint64_t have_dense;
+    char *const dscr = offer_align(scratch, scratch_bytes, &have_dense);
+    const bool dense = k > 0 && dscr && have_dense >= wbytes + uor_gfx950_suggested_scratch_i8(m, k, n) &&
                        (n + 127) / 128 <= 0x7FFFFFFFull && (k + 127) / 128 <= 65535ull &&
                        (k * (round_up(n, 16) / 16) + 255) / 256 <= 0x7FFFFFFFull;
     if (transposed && k > 0 && m <= 8 && k <= GEMV_MAX_K && (n + 3) / 4 <= 0x7FFFFFFFull) {
@@ -793,7 +797,7 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
     }
     if (dense) {
         const uint64_t ldw = round_up(n, 16);
-        int8_t *wt = (int8_t *)scratch;
+        int8_t *wt = (int8_t *)dscr;
         if (transposed) {
             const dim3 grid((unsigned)((n + 127) / 128), (unsigned)((k + 127) / 128));
             // One-byte codes of 4 or 8 elements in whole 16-byte row runs,
@@ -812,8 +816,8 @@ static int gemm_coded_impl(const uor_view *a, const uor_codec *codec, const void
         }
         UOR_HIP(hipGetLastError());
         const uor_view bv{wt, k * ldw, k, n, (int64_t)ldw, 1};
-        const int st2 = uor_gfx950_gemm_i8(a, &bv, c, out_type, alpha, beta, encode, (char *)scratch + wbytes,
-                                           scratch_bytes - wbytes, stream, route);
+        const int st2 = uor_gfx950_gemm_i8(a, &bv, c, out_type, alpha, beta, encode, dscr + wbytes,
+                                           have_dense - wbytes, stream, route);
         if (route && st2 == UOR_OK) {
             route->kind = UOR_ROUTE_CODED_DENSE;
             route->launches += 1;

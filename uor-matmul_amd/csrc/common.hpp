@@ -115,6 +115,19 @@ static inline void route_set(uor_route *r, int kind) {
     r->kind = kind;
 }
 
+// A scratch offer may start anywhere.  Every route carves it from its first
+// 256-byte aligned byte (so 8-byte atomics and 16-byte stores into it are
+// aligned); *have gets what is left of the offer from there (0 for none).
+static inline char *offer_align(void *scratch, uint64_t bytes, uint64_t *have) {
+    if (!scratch) {
+        *have = 0;
+        return nullptr;
+    }
+    const uintptr_t p0 = (uintptr_t)scratch, p1 = (p0 + 255) & ~(uintptr_t)255;
+    *have = bytes > (uint64_t)(p1 - p0) ? bytes - (uint64_t)(p1 - p0) : 0;
+    return (char *)p1;
+}
+
 // ------------------------------------------------------ integer epilogue --
 
 // The value range of an integer output of `bytes` bytes.

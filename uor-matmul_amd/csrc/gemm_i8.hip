@@ -1136,7 +1136,9 @@ extern "C" const char *uor_gfx950_status_string(int status) {
 
 extern "C" uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n) {
     (void)k;
-    return splitk_bytes(m, n);
+    // The partial sums, plus the slack that aligns an offer at any address.
+    const uint64_t b = splitk_bytes(m, n);
+    return b ? b + 256 : 0;
 }
 
 template <bool FAST>
@@ -1309,9 +1311,13 @@ extern "C" int uor_gfx950_gemm_i8(const uor_view *a, const uor_view *b, const uo
     if (st) return st;
     if (C.rows == 0 || C.cols == 0) return UOR_OK;
     hipStream_t s = (hipStream_t)stream;
+    // The split-K partial sums take 8-byte atomics: the offer from its first
+    // aligned byte.
+    uint64_t have;
+    char *work = offer_align(scratch, scratch_bytes, &have);
     if (fits_fast(out_type, A.cols, alpha, beta))
-        return run_i8<true>(A, B, C, out_type, alpha, beta, encode, scratch, scratch_bytes, s, route);
-    return run_i8<false>(A, B, C, out_type, alpha, beta, encode, scratch, scratch_bytes, s, route);
+        return run_i8<true>(A, B, C, out_type, alpha, beta, encode, work, have, s, route);
+    return run_i8<false>(A, B, C, out_type, alpha, beta, encode, work, have, s, route);
 }
 
 extern "C" int uor_gfx950_slice_gemm_ex_i8(uint64_t m, uint64_t k, uint64_t n, int64_t alpha,

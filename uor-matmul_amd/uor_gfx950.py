@@ -200,10 +200,36 @@ def _stream(stream):
     return torch.cuda.current_stream().cuda_stream
 
 
-def view(buf, rows, cols, rs, cs, rec=1):
-    """A uor_view over the flat device tensor `buf` (its length in elements
-    is buf.numel() // rec, for record types spelled as bytes)."""
-    return View(_ptr(buf), buf.numel() // rec, rows, cols, rs, cs)
+def _dev(buf):
+    """A buffer handed to the library must be device memory, contiguous."""
+    if buf is None:
+        return None
+    if not buf.is_cuda:
+        raise ValueError("uor_gfx950 buffers are device tensors")
+    if not buf.is_contiguous():
+        raise ValueError("uor_gfx950 buffers are contiguous tensors (strides go in the view)")
+    return buf
+
+
+def _len(buf, elem):
+    """The buffer's length in elements of `elem` bytes (the C side's element
+    type), whatever the tensor's own dtype: an int8 tensor passed as an i32
+    output holds a quarter as many elements as it has bytes."""
+    if buf is None:
+        return 0
+    return buf.numel() * buf.element_size() // elem
+
+
+def _nbytes(buf):
+    return 0 if buf is None else _dev(buf).numel() * buf.element_size()
+
+
+def view(buf, rows, cols, rs, cs, elem=1):
+    """A uor_view over the flat device tensor `buf` whose elements, as the
+    library reads them, are `elem` bytes (1 for i8, the output width for C, 2
+    for a Trop<i8> record, ...)."""
+    _dev(buf)
+    return View(_ptr(buf), _len(buf, elem), rows, cols, rs, cs)
 
 
 def gemm_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
@@ -211,33 +237,31 @@ def gemm_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
     """The view API at E = i8.  Returns (status, route dict).  `c` is a flat
     device tensor of the output type (int8/16/32/64, or int64 pairs for i128)."""
     ob = OUT[out]
-    rec = 2 if ob == 16 else 1
     av = view(a, *a_shape, *a_strides)
     bv = view(b, *b_shape, *b_strides)
-    cv = view(c, *c_shape, *c_strides, rec=rec)
+    cv = view(c, *c_shape, *c_strides, elem=ob)
     r = Route()
     st = lib().uor_gfx950_gemm_i8(ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob,
                                   int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
-                                  0 if scratch is None else scratch.numel() * scratch.element_size(),
-                                  _stream(stream), ctypes.byref(r))
+                                  _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
 
 
 def slice_gemm_ex_i8(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, out="i32", scratch=None,
                      stream=None):
     ob = OUT[out]
+    a, b, c = _dev(a), _dev(b), _dev(c)
     return lib().uor_gfx950_slice_gemm_ex_i8(
-        m, k, n, int(alpha), _ptr(a), a.numel(), lda, _ptr(b), b.numel(), ldb, int(beta),
-        _ptr(c), c.numel() // (2 if ob == 16 else 1), ldc, ob, _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+        m, k, n, int(alpha), _ptr(a), _len(a, 1), lda, _ptr(b), _len(b, 1), ldb, int(beta),
+        _ptr(c), _len(c, ob), ldc, ob, _ptr(scratch), _nbytes(scratch), _stream(stream))
 
 
 def slice_gemm_i8(m, k, n, a, b, c, out="i32", scratch=None, stream=None):
     ob = OUT[out]
+    a, b, c = _dev(a), _dev(b), _dev(c)
     return lib().uor_gfx950_slice_gemm_i8(
-        m, k, n, _ptr(a), a.numel(), _ptr(b), b.numel(), _ptr(c),
-        c.numel() // (2 if ob == 16 else 1), ob, _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+        m, k, n, _ptr(a), _len(a, 1), _ptr(b), _len(b, 1), _ptr(c), _len(c, ob), ob,
+        _ptr(scratch), _nbytes(scratch), _stream(stream))
 
 
 def suggested_scratch_i8(m, k, n):
@@ -251,15 +275,13 @@ def gemm_int(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides
     type (int8/16/32/64, or int64 pairs for i128)."""
     eb = a.element_size()
     ob = OUT[out]
-    rec = 2 if ob == 16 else 1
-    av = view(a, *a_shape, *a_strides)
-    bv = view(b, *b_shape, *b_strides)
-    cv = view(c, *c_shape, *c_strides, rec=rec)
+    av = view(a, *a_shape, *a_strides, elem=eb)
+    bv = view(b, *b_shape, *b_strides, elem=eb)
+    cv = view(c, *c_shape, *c_strides, elem=ob)
     r = Route()
     st = lib().uor_gfx950_gemm_int(eb, ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob,
                                    int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
-                                   0 if scratch is None else scratch.numel() * scratch.element_size(),
-                                   _stream(stream), ctypes.byref(r))
+                                   _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
 
 
@@ -271,13 +293,13 @@ def gemm_lut4(a, m, k, a_strides, codes, n, books, group, c, c_strides, out="i32
               beta=0, encode="nearest", scratch=None, stream=None):
     ob = OUT[out]
     av = view(a, m, k, *a_strides)
-    cv = view(c, m, n, *c_strides, rec=2 if ob == 16 else 1)
+    cv = view(c, m, n, *c_strides, elem=ob)
+    codes, books = _dev(codes), _dev(books)
     r = Route()
     st = lib().uor_gfx950_gemm_lut4(
-        ctypes.byref(av), _ptr(codes), codes.numel(), n, _ptr(books), books.numel(), group,
+        ctypes.byref(av), _ptr(codes), _len(codes, 1), n, _ptr(books), _len(books, 1), group,
         ctypes.byref(cv), ob, int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
-        ctypes.byref(r))
+        _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
 
 
@@ -289,24 +311,25 @@ def gemm_float(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strid
                beta=0, encode="nearest", scratch=None, stream=None):
     import torch
     is64 = int(a.dtype == torch.float64)
-    av = view(a, *a_shape, *a_strides)
-    bv = view(b, *b_shape, *b_strides)
-    cv = view(c, *c_shape, *c_strides)
+    es = 8 if is64 else 4
+    av = view(a, *a_shape, *a_strides, elem=es)
+    bv = view(b, *b_shape, *b_strides, elem=es)
+    cv = view(c, *c_shape, *c_strides, elem=es)
     r = Route()
     st = lib().uor_gfx950_gemm_float(
         is64, ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), int(alpha), int(beta),
-        ENCODE[encode], _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
-        ctypes.byref(r))
+        ENCODE[encode], _ptr(scratch), _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
 
 
 def slice_gemm_float_ex(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, scratch=None, stream=None):
     import torch
+    is64 = int(a.dtype == torch.float64)
+    es = 8 if is64 else 4
+    a, b, c = _dev(a), _dev(b), _dev(c)
     return lib().uor_gfx950_slice_gemm_float_ex(
-        int(a.dtype == torch.float64), m, k, n, int(alpha), _ptr(a), a.numel(), lda, _ptr(b),
-        b.numel(), ldb, int(beta), _ptr(c), c.numel(), ldc, _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+        is64, m, k, n, int(alpha), _ptr(a), _len(a, es), lda, _ptr(b), _len(b, es), ldb,
+        int(beta), _ptr(c), _len(c, es), ldc, _ptr(scratch), _nbytes(scratch), _stream(stream))
 
 
 def raw_gemm(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, a_off=0, b_off=0,
@@ -319,7 +342,7 @@ def raw_gemm(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, a_off=
     f = lib().uor_gfx950_dgemm if is64 else lib().uor_gfx950_sgemm
     return f(m, k, n, int(alpha), a.data_ptr() + a_off * es, rsa, csa, b.data_ptr() + b_off * es,
              rsb, csb, int(beta), c.data_ptr() + c_off * es, rsc, csc, _ptr(scratch),
-             0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream))
+             _nbytes(scratch), _stream(stream))
 
 
 def suggested_scratch_float(is64, m, k, n):
@@ -330,15 +353,14 @@ def gemm_trop_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_str
                  alpha=(0, True), beta=(0, False), encode="nearest", scratch=None, stream=None):
     """a, b: uint8 device tensors of 2-byte Trop<i8> records; c: uint8 tensor of
     2*out-byte Trop<out> records."""
-    av = view(a, *a_shape, *a_strides, rec=2)
-    bv = view(b, *b_shape, *b_strides, rec=2)
-    cv = view(c, *c_shape, *c_strides, rec=2 * out)
+    av = view(a, *a_shape, *a_strides, elem=2)
+    bv = view(b, *b_shape, *b_strides, elem=2)
+    cv = view(c, *c_shape, *c_strides, elem=2 * out)
     r = Route()
     st = lib().uor_gfx950_gemm_trop_i8(
         ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), out, int(alpha[0]),
         int(bool(alpha[1])), int(beta[0]), int(bool(beta[1])), ENCODE[encode], _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
-        ctypes.byref(r))
+        _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
 
 
@@ -348,16 +370,15 @@ def gemm_trop_i8_selected(a, a_shape, a_strides, b, b_shape, b_strides, c, c_sha
     """gemm_selected at E = Trop<i8>: as gemm_trop_i8, plus the witness `w`, a
     flat int64/uint64 device tensor viewed as w_shape (default c_shape) with
     w_strides."""
-    av = view(a, *a_shape, *a_strides, rec=2)
-    bv = view(b, *b_shape, *b_strides, rec=2)
-    cv = view(c, *c_shape, *c_strides, rec=2 * out)
-    wv = view(w, *(w_shape or c_shape), *w_strides)
+    av = view(a, *a_shape, *a_strides, elem=2)
+    bv = view(b, *b_shape, *b_strides, elem=2)
+    cv = view(c, *c_shape, *c_strides, elem=2 * out)
+    wv = view(w, *(w_shape or c_shape), *w_strides, elem=8)
     r = Route()
     st = lib().uor_gfx950_gemm_trop_i8_selected(
         ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ctypes.byref(wv), out,
         int(alpha[0]), int(bool(alpha[1])), int(beta[0]), int(bool(beta[1])), ENCODE[encode],
-        WITNESS.get(mechanism, mechanism), _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        WITNESS.get(mechanism, mechanism), _ptr(scratch), _nbytes(scratch), _stream(stream),
         ctypes.byref(r))
     return st, r.as_dict()
 
@@ -381,16 +402,17 @@ def gemm_coded(a, a_shape, a_strides, cd, codes, w_rows, w_cols, transposed, c, 
     W a fixed-width coded operand: `codes` is a device tensor of the stored
     codes (uint8, or int16/uint16 for 16-bit codes)."""
     ob = OUT[out]
-    rec = 2 if ob == 16 else 1
     av = view(a, *a_shape, *a_strides)
-    cv = view(c, *c_shape, *c_strides, rec=rec)
+    cv = view(c, *c_shape, *c_strides, elem=ob)
+    # Stored codes are bytes when packed, else code_bits / 8 bytes each.
+    celem = 1 if cd.packed else max(1, cd.code_bits // 8)
+    codes = _dev(codes)
     r = Route()
     f = lib().uor_gfx950_gemm_coded_collapsed if collapse else lib().uor_gfx950_gemm_coded
     st = f(
-        ctypes.byref(av), ctypes.byref(cd), _ptr(codes), codes.numel(), w_rows, w_cols,
+        ctypes.byref(av), ctypes.byref(cd), _ptr(codes), _len(codes, celem), w_rows, w_cols,
         int(bool(transposed)), ctypes.byref(cv), ob, int(alpha), int(beta), ENCODE[encode],
-        _ptr(scratch), 0 if scratch is None else scratch.numel() * scratch.element_size(),
-        _stream(stream), ctypes.byref(r))
+        _ptr(scratch), _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
 
 
@@ -406,12 +428,11 @@ def gemm_collapsed_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, 
     ob = OUT[out]
     av = view(a, *a_shape, *a_strides)
     bv = view(b, *b_shape, *b_strides)
-    cv = view(c, *c_shape, *c_strides, rec=2 if ob == 16 else 1)
+    cv = view(c, *c_shape, *c_strides, elem=ob)
     r = Route()
     st = lib().uor_gfx950_gemm_collapsed_i8(
         ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob, int(alpha), int(beta),
-        ENCODE[encode], int(bool(columns)), _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        ENCODE[encode], int(bool(columns)), _ptr(scratch), _nbytes(scratch), _stream(stream),
         ctypes.byref(r))
     return st, r.as_dict()
 
@@ -430,15 +451,16 @@ def gemm_coded_float(a, a_shape, a_strides, table, codes, w_rows, w_cols, transp
     float64 device tensor (the codebook), `codes` uint8 or int16 (u16 codes)."""
     import torch
     is64 = int(a.dtype == torch.float64)
-    av = view(a, *a_shape, *a_strides)
-    cv = view(c, *c_shape, *c_strides)
+    es = 8 if is64 else 4
+    av = view(a, *a_shape, *a_strides, elem=es)
+    cv = view(c, *c_shape, *c_strides, elem=es)
     bits = 8 if codes.element_size() == 1 else 16
+    table, codes = _dev(table), _dev(codes)
     r = Route()
     st = lib().uor_gfx950_gemm_coded_float(
-        is64, ctypes.byref(av), _ptr(table), table.numel(), bits, _ptr(codes), codes.numel(),
-        w_rows, w_cols, int(bool(transposed)), ctypes.byref(cv), int(alpha), int(beta),
-        ENCODE[encode], _ptr(scratch),
-        0 if scratch is None else scratch.numel() * scratch.element_size(), _stream(stream),
+        is64, ctypes.byref(av), _ptr(table), _len(table, es), bits, _ptr(codes),
+        _len(codes, bits // 8), w_rows, w_cols, int(bool(transposed)), ctypes.byref(cv),
+        int(alpha), int(beta), ENCODE[encode], _ptr(scratch), _nbytes(scratch), _stream(stream),
         ctypes.byref(r))
     return st, r.as_dict()
 
