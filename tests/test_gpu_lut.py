@@ -71,17 +71,62 @@ def test_epilogue(oracle, uor, dev, out, encode, m):
                  encode=encode)
 
 
+TILE = (8, 16)  # route["split_k"] of the 16-column tile kernel (its waves per workgroup)
+
+
 @pytest.mark.parametrize("out", [np.int8, np.int16, np.int32, np.int64])
 @pytest.mark.parametrize("encode", ["nearest", "wrapping"])
-def test_lds_kernel_epilogue(oracle, uor, dev, out, encode):
-    """The LDS-activation kernel's output paths (k % 2048 == 0, 2 <= m <=
-    32): i32 rows in 16-byte stores except the ragged last columns (n = 45),
+@pytest.mark.parametrize("k", [2048, 16384])
+def test_lds_and_tile_kernel_epilogue(oracle, uor, dev, out, encode, k):
+    """The output paths of the 16-column tile kernel (k = 2048: a multiple of
+    2048 up to 8192, m <= 16) and of the LDS-activation kernel (k = 16384,
+    2 <= m <= 32): i32 rows in 16-byte stores except the ragged last columns (n = 45),
     the per-cell finish for the other widths, each with plain, scaled and
     saturating alpha/beta."""
     for alpha, beta in [(1, 0), (3, -1), (1 << 40, -(1 << 35))]:
-        route = run_case(oracle, uor, dev, 9, 2048, 45, 8, seed=13, out=out, alpha=alpha,
+        route = run_case(oracle, uor, dev, 9, k, 45, 8, seed=13, out=out, alpha=alpha,
                          beta=beta, encode=encode)
-        assert route["kind"] == "lut4_mfma" and route["split_k"] == 1, route
+        assert route["kind"] == "lut4_mfma", route
+        assert (route["split_k"] in TILE) == (k <= 8192), route
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 32])
+@pytest.mark.parametrize("k", [2048, 4096, 6144, 8192])
+def test_tile_kernel_against_oracle(oracle, uor, dev, m, k):
+    """The 16-column tile kernel (one or two row blocks) at every depth it takes: ragged
+    n (a last tile of 3 columns), codebook groups that are not a multiple of
+    the 16-column tile (7) or are single columns, alpha/beta and the i64
+    epilogue, against the oracle."""
+    for n, group, out, alpha, beta in [(35, 7, np.int32, 1, 0), (50, 1, np.int64, -3, 2),
+                                       (64, 128, np.int32, 5, -1)]:
+        route = run_case(oracle, uor, dev, m, k, n, group, seed=m * 31 + k + n, out=out,
+                         alpha=alpha, beta=beta)
+        assert route["kind"] == "lut4_mfma" and route["split_k"] in TILE, route
+
+
+@pytest.mark.parametrize("m,k,n,group", [(1, 8192, 28672, 128), (8, 8192, 40000 + 9, 64),
+                                         (32, 8192, 28672, 128), (24, 4096, 12 * 256 * 16, 128),
+                                         (3, 2048, 16 * 100 + 1, 16), (12, 8192, 256 * 16, 3),
+                                         (16, 4096, 12 * 256 * 16 + 16, 128)])
+def test_tile_kernel_tiles_per_workgroup(uor, dev, m, k, n, group):
+    """The tile kernel with 7, 10 and 12 tiles per workgroup (the most whose
+    sums it holds), fewer tiles than CUs, one tile per CU, and one tile past
+    its limit (another kernel then); against a decode in torch plus a float64
+    matmul (exact: every sum is an integer below 2^53)."""
+    rng = np.random.default_rng(m + k + n)
+    a = to_dev(rng.integers(-128, 128, m * k).astype(np.int8), dev)
+    codes = to_dev(rng.integers(0, 256, n * k // 2).astype(np.uint8), dev)
+    books = to_dev(rng.integers(-128, 128, ((n + group - 1) // group) * 16).astype(np.int8), dev)
+    c = torch.full((m * n,), 7, dtype=torch.int32, device=dev)
+    st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1))
+    torch.cuda.synchronize()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiled = (n + 15) // 16 <= 12 * cus
+    assert st == 0 and route["kind"] == "lut4_mfma", route
+    assert (route["split_k"] in TILE) == tiled, route
+    W = decode_torch(codes, n, k, books, group).to(torch.float64)
+    want = a.view(m, k).to(torch.float64) @ W.T
+    assert torch.equal(c.view(m, n).to(torch.float64), want), route
 
 
 def test_deep_rows_fold_exactly(oracle, uor, dev):
@@ -149,12 +194,14 @@ def test_mfma16_quarters_at_depth_limit(uor, dev, k):
 
 @pytest.mark.parametrize("m,k,n", [(8, 4096, 8192 - 5), (20, 2048, 12288 + 3), (13, 2048, 32768),
                                    (32, 2048, 28672), (5, 6144, 16 * 256 * 5 + 9), (32, 2048, 64),
-                                   (2, 8192, 28672), (4, 2048, 1000)])
+                                   (2, 8192, 28672), (4, 2048, 1000), (8, 16384, 8192 - 5),
+                                   (32, 10240, 4096 + 3)])
 def test_tiles_per_cu(uor, dev, m, k, n):
-    """The LDS-activation kernel (2 <= m <= 32) with 2, 4, 8, 7, 6, 1, 7 and
-    1 sixteen-column tiles per CU (ragged n, one row block or two, one to
-    three activation chunks), against a decode in torch plus a float64 matmul
-    (exact: every sum is an integer below 2^53)."""
+    """2 <= m <= 32 with 2, 4, 8, 7, 6, 1, 7 and 1 sixteen-column tiles per
+    CU (ragged n, one row block or two): the code-stream kernel up to
+    k = 8192, the LDS-activation kernel beyond (one to five activation
+    chunks), against a decode in torch plus a float64 matmul (exact: every
+    sum is an integer below 2^53)."""
     group = 128
     rng = np.random.default_rng(m + k + n)
     a = to_dev(rng.integers(-128, 128, m * k).astype(np.int8), dev)
@@ -163,7 +210,8 @@ def test_tiles_per_cu(uor, dev, m, k, n):
     c = torch.zeros(m * n, dtype=torch.int32, device=dev)
     st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1))
     torch.cuda.synchronize()
-    assert st == 0 and route["kind"] == "lut4_mfma" and route["split_k"] == 1, route
+    assert st == 0 and route["kind"] == "lut4_mfma", route
+    assert (route["split_k"] in TILE) == (k <= 8192), route
     W = decode_torch(codes, n, k, books, group).to(torch.float64)
     want = a.view(m, k).to(torch.float64) @ W.T
     assert torch.equal(c.view(m, n).to(torch.float64), want), route

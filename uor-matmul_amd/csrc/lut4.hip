@@ -21,6 +21,7 @@
 // the codes dominate at decode shapes, so the kernels are built to stream
 // them: every code byte is read from HBM exactly once.
 
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -382,6 +383,26 @@ static int device_cus_lut() {
         return n;
     }();
     return cus;
+}
+
+// The 16-column tile kernel for the decode shapes (UOR_GFX950_LUT_TILE=off
+// turns it off, for measuring the kernels it replaced).
+static bool lut_tile_on() {
+    static bool on = [] {
+        const char *e = getenv("UOR_GFX950_LUT_TILE");
+        return !(e && !strcmp(e, "off"));
+    }();
+    return on;
+}
+// Waves per workgroup of the tile kernel (UOR_GFX950_LUT_TILE=8 or 16, for
+// measurement; 16, the default, measured 23.3 against 24.7 us at m = 1 and
+// the config weights).
+static int lut_tile_waves() {
+    static int w = [] {
+        const char *e = getenv("UOR_GFX950_LUT_TILE");
+        return (e && !strcmp(e, "8")) ? 8 : 16;
+    }();
+    return w;
 }
 
 static int lut_variant() {
@@ -774,6 +795,246 @@ __global__ void __launch_bounds__(512) lut4_lds_kernel(LutArgs L, int book_align
     }
 }
 
+// ------------------------- 1 <= m <= 32: 16-column tiles through LDS, MFMA
+//
+// The decode shapes read every code byte once and little else, so this
+// kernel is built around the code stream.  HBM served it best (measured over
+// load patterns, in-flight depths and wave counts on MI355X) when each CU
+// reads one contiguous 16-column tile (64 KiB at k = 8192) at a time with
+// nothing else in flight: one workgroup of 16 waves per CU owns the tiles
+// t = b, b + G, b + 2G, ... (G workgroups: the chip reads a window of G
+// consecutive tiles); wave w loads column w of the next tile -- k/2
+// consecutive bytes, 1 KiB per load (16 bytes per lane, non-temporal: the
+// codes are read once) -- after computing the current one, and stores it
+// into the other of two LDS tile buffers; one barrier per tile.
+//
+// Compute: wave w takes weights [w*k/16, (w+1)*k/16) of every column of the
+// tile.  Lane (c = l%16, g = l/16) reads column c's 16 code bytes for
+// weights [32*(4*KQ*w + 4p + g), +32) per pair p (ds_read_b128), giving two
+// v_mfma_i32_16x16x64_i8 A operands (weights +0..16 and +16..32).  The wave's
+// activations for its weight range sit in registers for the whole kernel,
+// already in the decode's order ([a0 a2 a4 a6 | a1 a3 a5 a7 | a8 .. a14 |
+// a9 .. a15] per 16-byte operand), so a code dword costs the 13 VALU ops of
+// decode8 and nothing else; rows past m are zero B operands.  The waves' i32
+// partials of a tile meet in LDS through ds_add (exact: |sum| <= k * 2^14 <
+// 2^31), and the workgroup finishes its (at most NTB) tiles at the end.
+//
+// LDS: column c's 16-byte chunk x lands at slot x ^ c, so the 16 lanes of a
+// ds_read_b128 phase (one chunk index, 16 columns) hit 16 distinct slots.
+constexpr int LT_NTB = 12;  // tiles per workgroup at most (their sums stay in LDS)
+
+typedef __attribute__((address_space(1))) const v4i global_v4i_c;
+typedef __attribute__((address_space(3))) const v4i lds_v4i_c;
+typedef __attribute__((address_space(3))) v4i lds_v4i;
+
+// A 16-byte non-temporal global load (global_load_dwordx4 ... nt: the
+// address space is explicit so the compiler never falls back to a flat load,
+// whose lgkmcnt share would make every LDS wait also wait for it).
+__device__ inline v4i ld_nt16(const void *p) { return __builtin_nontemporal_load((global_v4i_c *)p); }
+__device__ inline v4i lds_rd16(uint32_t a) { return *(lds_v4i_c *)(uintptr_t)a; }
+// ds_read_b128 the compiler neither moves nor waits for (the caller waits with
+// s_waitcnt lgkmcnt and then takes the registers over).
+__device__ inline v4i lds_rd16_asm(uint32_t a) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ inline void lds_wr16(uint32_t a, v4i v) { *(lds_v4i *)(uintptr_t)a = v; }
+// LDS writes done, then the workgroup barrier (no wait on the loads in
+// flight, which a memory fence would add).
+__device__ inline void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Finish the batch of tiles [t0, t0 + cnt) of workgroup b (tiles b + G*i)
+// from the tile sums in LDS: 4 consecutive columns per item.
+template <int ROWS, int TSW>
+__device__ __attribute__((noinline)) void lut_tile_finish(char *cbase, int64_t crs, int64_t ccs, int ob, int64_t alpha,
+                                                          int64_t beta, int mode, uint64_t m, uint64_t n,
+                                                          const int *tsum, uint32_t b, uint32_t G, uint32_t t0,
+                                                          uint32_t cnt) {
+    LutArgs L{};
+    L.c = cbase;
+    L.crs = crs;
+    L.ccs = ccs;
+    L.ob = ob;
+    L.alpha = alpha;
+    L.beta = beta;
+    L.mode = mode;
+    const bool vec = ob == 4 && ccs == 1 && ((uintptr_t)cbase & 15) == 0 && (crs & 3) == 0 && alpha == 1 && beta == 0;
+    for (uint32_t e = threadIdx.x; e < cnt * ROWS * 4; e += blockDim.x) {
+        const uint32_t sl = e / (ROWS * 4), row = (e / 4) % ROWS, c4 = e % 4;
+        if (row >= m) continue;
+        const uint64_t col0 = (uint64_t)(b + G * (t0 + sl)) * 16 + 4 * c4;
+        const int *ts = &tsum[(sl * ROWS + row) * TSW + 4 * c4];
+        if (vec && col0 + 4 <= n) {
+            *(v4i *)((int32_t *)cbase + (int64_t)row * crs + (int64_t)col0) = v4i{ts[0], ts[1], ts[2], ts[3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (col0 + i < n) lut_finish_any(L, row, col0 + i, (int64_t)ts[i]);
+        }
+    }
+}
+
+template <int MB, int KQ, int W>
+__global__ void __launch_bounds__(64 * W) lut4_tile_kernel(LutArgs L, uint32_t ntiles) {
+    constexpr int ROWS = 16 * MB;
+    constexpr int TSW = 17;              // words per tile-sum row (16 columns + pad)
+    constexpr int CB = KQ * 1024;        // code bytes per column (k / 2)
+    constexpr int TB = 16 * CB;          // code bytes per tile
+    constexpr int NT = W * 64;           // threads
+    constexpr int CPW = 16 / W;          // columns each wave loads per tile
+    constexpr int PW = CPW * KQ;         // 1 KiB pieces each wave loads per tile
+    constexpr int NP = 16 * KQ / W;      // 128-weight pairs each wave computes per column
+    __shared__ __attribute__((aligned(16))) uint8_t tbuf[2 * TB];
+    __shared__ int tsum[LT_NTB * ROWS * TSW];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t ntl = b < ntiles ? (ntiles - 1 - b) / G + 1 : 0;  // this workgroup's tiles
+    if (ntl == 0) return;
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+    const uint64_t n = L.n, m = L.m, half = L.half, group = L.group;
+    const uint8_t *const codes = L.codes;
+    const int8_t *const books = L.books;
+    const uint32_t tb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)tbuf;
+
+    // Activations in the decode's order: act[p][h][b] covers row 16b + c,
+    // weights w*k/W + 128p + 32g + 16h + [0, 16).  Rows past m read row m-1
+    // and are zeroed.
+    v4i act[NP][2][MB];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int bb = 0; bb < MB; ++bb) {
+                const uint64_t r = 16 * bb + c < m ? 16 * bb + c : m - 1;
+                const uint64_t kk = (uint64_t)(128 * NP) * wave + 128 * p + 32 * g + 16 * h;
+                act[p][h][bb] = *(global_v4i_c *)(L.a + (int64_t)r * L.ars + (int64_t)kk);
+            }
+    // Column c's codebook of tile i (16 bytes; a ragged tile's missing
+    // columns read the last column's).
+#define UOR_LT_BOOK(I)                                                                         \
+    ([&]() -> v4i {                                                                            \
+        uint64_t j_ = (uint64_t)(b + G * (I)) * 16 + c;                                        \
+        if (j_ >= n) j_ = n - 1;                                                               \
+        return *(global_v4i_c *)(books + (j_ / group) * 16);                                   \
+    }())
+    // This wave's piece e of tile i: column CPW*w + e / KQ, bytes
+    // [1024 * (e % KQ), +1024), lane l's 16 bytes at +16l (the wave's pieces
+    // are consecutive bytes).  A ragged last tile re-reads a valid row
+    // (never stored).
+#define UOR_LT_PIECE(I, E)                                                                     \
+    ([&]() -> const uint8_t * {                                                               \
+        uint64_t j_ = (uint64_t)(b + G * (I)) * 16 + CPW * wave + (E) / KQ;                    \
+        if (j_ >= n) j_ = n - 1;                                                               \
+        return codes + j_ * half + 1024 * ((E) % KQ) + 16 * lane;                              \
+    }())
+    // Lane l stores chunk 64q + l of column cc at slot (64q + l) ^ cc.
+#define UOR_LT_STORE(BUF, E, V)                                                                \
+    {                                                                                          \
+        const uint32_t cc_ = (uint32_t)(CPW * wave + (E) / KQ);                                \
+        lds_wr16((BUF) + cc_ * CB + 16u * ((64u * ((E) % KQ) + lane) ^ cc_), (V));             \
+    }
+
+    v4i bk = UOR_LT_BOOK(0u);
+    v4i ring[PW];
+#pragma unroll
+    for (int e = 0; e < PW; ++e) ring[e] = ld_nt16(UOR_LT_PIECE(0u, e));
+    for (int e = threadIdx.x; e < LT_NTB * ROWS * TSW; e += NT) tsum[e] = 0;
+    // Activations into the decode's order (rows past m zero).
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int bb = 0; bb < MB; ++bb) {
+                v4i x = act[p][h][bb];
+                if ((uint64_t)(16 * bb + c) >= m) x = v4i{0, 0, 0, 0};
+                act[p][h][bb] = v4i{(int)perm(x[1], x[0], 0x06040200u), (int)perm(x[1], x[0], 0x07050301u),
+                                    (int)perm(x[3], x[2], 0x06040200u), (int)perm(x[3], x[2], 0x07050301u)};
+            }
+    // Tile 0 into its buffer, tile 1 requested.
+#pragma unroll
+    for (int e = 0; e < PW; ++e) {
+        UOR_LT_STORE(tb0, e, ring[e])
+        if (ntl > 1) ring[e] = ld_nt16(UOR_LT_PIECE(1u, e));
+    }
+    lds_barrier();
+
+    // Iteration i computes tile i, then stores tile i+1 (its pieces arrived
+    // in `ring` meanwhile) into the other buffer and requests tile i+2.
+    // NEXT: tile i+1 exists; AFTER: tile i+2 does (the loads per iteration
+    // are then the same everywhere, and the compiler's waits stay exact).
+#define UOR_LT_ITER(I, NEXT, AFTER)                                                            \
+    {                                                                                          \
+        const uint32_t i_ = (I);                                                               \
+        const uint32_t cur = tb0 + (i_ & 1) * TB, nxt = tb0 + ((i_ + 1) & 1) * TB;             \
+        const uint32_t q0 = (uint32_t)bk[0], q1 = (uint32_t)bk[1], q2 = (uint32_t)bk[2],       \
+                       q3 = (uint32_t)bk[3];                                                   \
+        if (NEXT) bk = UOR_LT_BOOK(i_ + 1);                                                    \
+        /* All of the wave's code chunks first (their LDS latencies overlap), */             \
+        /* then decode and MFMA into two accumulator chains per row block. */                   \
+        /* (as asm: the scheduler would otherwise sink each read next to its */               \
+        /* use and wait for it there) */                                                       \
+        /* (with two row blocks the registers are short: there the compiler */                \
+        /* places the reads) */                                                                \
+        v4i cw[NP];                                                                            \
+        _Pragma("unroll") for (int p = 0; p < NP; ++p) {                                       \
+            const uint32_t x = (uint32_t)(4 * NP * wave + 4 * p + g);                          \
+            const uint32_t a_ = cur + (uint32_t)c * CB + 16u * (x ^ (uint32_t)c);               \
+            cw[p] = MB == 1 ? lds_rd16_asm(a_) : lds_rd16(a_);                                 \
+        }                                                                                      \
+        if (MB == 1) {                                                                         \
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                \
+            _Pragma("unroll") for (int p = 0; p < NP; ++p) asm volatile("" : "+v"(cw[p]));      \
+        }                                                                                      \
+        constexpr int CH = MB == 1 ? 2 : 1; /* independent MFMA chains per row block */      \
+        v4i acc[CH][MB];                                                                       \
+        _Pragma("unroll") for (int ch = 0; ch < CH; ++ch)                                      \
+            _Pragma("unroll") for (int bb = 0; bb < MB; ++bb) acc[ch][bb] = v4i{0, 0, 0, 0};   \
+        _Pragma("unroll") for (int p = 0; p < NP; ++p) {                                       \
+            _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                    \
+                uint32_t e0, o0, e1, o1;                                                       \
+                decode8((uint32_t)cw[p][2 * h], q0, q1, q2, q3, m4, id, e0, o0);               \
+                decode8((uint32_t)cw[p][2 * h + 1], q0, q1, q2, q3, m4, id, e1, o1);           \
+                const v4i wop = v4i{(int)e0, (int)o0, (int)e1, (int)o1};                       \
+                _Pragma("unroll") for (int bb = 0; bb < MB; ++bb) acc[h % CH][bb] =            \
+                    __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, act[p][h][bb], acc[h % CH][bb], 0, 0, 0); \
+            }                                                                                  \
+        }                                                                                      \
+        _Pragma("unroll") for (int bb = 0; bb < MB; ++bb)                                      \
+            _Pragma("unroll") for (int v = 0; v < 4; ++v)                                      \
+                atomicAdd(&tsum[(i_ * ROWS + 16 * bb + c) * TSW + 4 * g + v],                  \
+                          acc[0][bb][v] + (CH > 1 ? acc[CH - 1][bb][v] : 0));                  \
+        if (NEXT) {                                                                            \
+            _Pragma("unroll") for (int e = 0; e < PW; ++e) {                                   \
+                UOR_LT_STORE(nxt, e, ring[e])                                                  \
+                if (AFTER) ring[e] = ld_nt16(UOR_LT_PIECE(i_ + 2, e));                         \
+            }                                                                                  \
+        }                                                                                      \
+        lds_barrier();                                                                         \
+    }
+    uint32_t i = 0;
+    for (; i + 2 < ntl; ++i) UOR_LT_ITER(i, true, true)
+    if (i + 1 < ntl) {
+        UOR_LT_ITER(i, true, false)
+        ++i;
+    }
+    UOR_LT_ITER(i, false, false)
+    lut_tile_finish<ROWS, TSW>(L.c, L.crs, L.ccs, L.ob, L.alpha, L.beta, L.mode, m, n, tsum, b, G, 0, ntl);
+#undef UOR_LT_ITER
+#undef UOR_LT_STORE
+#undef UOR_LT_PIECE
+#undef UOR_LT_BOOK
+}
+
 // ------------------------------------------- many rows: decode, then dense
 //
 // For m >= LUT_PREFILL_M (or m >= 80 at k >= 4096, where the dense route
@@ -899,6 +1160,43 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
                 route->scratch_used += wbytes;
             }
             return st2;
+        }
+    }
+    // 1 <= m <= 32, k a multiple of 2048 up to 8192 (a wave's activations
+    // fit its registers), at most LT_NTB tiles per CU (their sums fit LDS),
+    // 16-byte aligned code and activation rows and codebooks: the 16-column
+    // tiles through LDS, one workgroup per CU.
+    if (m <= 32 && k % 2048 == 0 && k >= 2048 && k <= 8192 && code_fast && a16 &&
+        ((uintptr_t)books & 15) == 0 && lut_tile_on()) {
+        const uint64_t ntiles = (n + 15) / 16;
+        const uint64_t cus = (uint64_t)device_cus_lut();
+        if ((ntiles + cus - 1) / cus <= (uint64_t)LT_NTB) {
+            const unsigned G = (unsigned)std::min<uint64_t>(cus, ntiles);
+            const int w = lut_tile_waves();
+            if (route) route->tile_m = m <= 16 ? 16 : 32, route->tile_n = 16, route->tile_k = (int)(k / w),
+                       route->split_k = w, route->kind = UOR_ROUTE_LUT4_MFMA;
+#define UOR_LT(MB, KQ)                                                                                       \
+    if (w == 16) hipLaunchKernelGGL((lut4_tile_kernel<MB, KQ, 16>), dim3(G), dim3(1024), 0, s, L, (uint32_t)ntiles); \
+    else hipLaunchKernelGGL((lut4_tile_kernel<MB, KQ, 8>), dim3(G), dim3(512), 0, s, L, (uint32_t)ntiles);
+            const int kq = (int)(k / 2048);
+            if (m <= 16) {
+                switch (kq) {
+                case 1: UOR_LT(1, 1); break;
+                case 2: UOR_LT(1, 2); break;
+                case 3: UOR_LT(1, 3); break;
+                default: UOR_LT(1, 4); break;
+                }
+            } else {
+                switch (kq) {
+                case 1: UOR_LT(2, 1); break;
+                case 2: UOR_LT(2, 2); break;
+                case 3: UOR_LT(2, 3); break;
+                default: UOR_LT(2, 4); break;
+                }
+            }
+#undef UOR_LT
+            UOR_HIP(hipGetLastError());
+            return UOR_OK;
         }
     }
     // 2 <= m <= 32, whole 2048-weight blocks, k <= 65536 (each wave's i32 sum
