@@ -21,8 +21,9 @@
  *     (crates/uor-matmul-core/src/error.rs:28-53) as 1 and 2; a buffer that
  *     does not hold the view its caller described (MatView::new -> None,
  *     layout.rs:212; the slice face's does_not_fit panic, slice.rs:104-116)
- *     as 3; an argument outside the enums below as 4; a HIP runtime failure
- *     as 100 + hipError_t (device-only; the reference has no such state).
+ *     as 3; an argument outside the enums below as 4; a request beyond the
+ *     no-alloc entry's static scratch as 5; a HIP runtime failure as
+ *     100 + hipError_t (device-only; the reference has no such state).
  *     Values, depth and magnitude never produce an error (reference CT-01,
  *     CT-05).
  */
@@ -42,6 +43,8 @@ extern "C" {
 #define UOR_OUTPUT_ALIASES_ITSELF 2  /* NotAProduct::OutputAliasesItself */
 #define UOR_SHORT_BUFFER 3           /* a view does not fit its buffer */
 #define UOR_INVALID_ARGUMENT 4       /* unknown enum value */
+#define UOR_SCRATCH_LIMIT 5          /* uor_gfx950_gemm_i8_noalloc: the call needs more
+                                        scratch than UOR_NOALLOC_SCRATCH_BYTES */
 #define UOR_HIP_ERROR 100            /* + hipError_t */
 
 /* EncodeMode, crates/uor-matmul-core/src/policy.rs:19-43.  The slice face
@@ -158,6 +161,23 @@ int uor_gfx950_slice_gemm_i8(uint64_t m, uint64_t k, uint64_t n,
  * reference's figure sizes CPU panels, which this route does not use.
  */
 uint64_t uor_gfx950_suggested_scratch_i8(uint64_t m, uint64_t k, uint64_t n);
+
+/*
+ * uor_gfx950_gemm_i8 without a scratch offer and without any allocation: no
+ * counterpart in the reference.  It is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The scratch is a static device array of
+ * UOR_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call
+ * whose fastest route needs more (the split-K partial sums, m*n*8 bytes, taken
+ * when k > 65536 or the output is small at k >= 8192) returns
+ * UOR_SCRATCH_LIMIT.  Same bytes as uor_gfx950_gemm_i8.  Calls that overlap on
+ * one GPU share its array and race: order them on one stream.  The first call
+ * on a device looks the array's device address up (hipGetSymbolAddress).
+ */
+#define UOR_NOALLOC_SCRATCH_BYTES (16u << 20)
+int uor_gfx950_gemm_i8_noalloc(const uor_view *a, const uor_view *b, const uor_view *c,
+                               int out_type, int64_t alpha, int64_t beta, int encode,
+                               void *stream, uor_route *route);
 
 /*
  * The view API at E = i16, i32, i64 (elem_bytes 2, 4, 8; 1 forwards to

@@ -25,6 +25,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include <type_traits>
 
 #include "mfma_dl.hpp"
@@ -1130,6 +1132,7 @@ extern "C" const char *uor_gfx950_status_string(int status) {
     case UOR_OUTPUT_ALIASES_ITSELF: return "output_aliases_itself";
     case UOR_SHORT_BUFFER: return "short_buffer";
     case UOR_INVALID_ARGUMENT: return "invalid_argument";
+    case UOR_SCRATCH_LIMIT: return "scratch_limit";
     default: return status >= UOR_HIP_ERROR ? "hip_error" : "unknown";
     }
 }
@@ -1340,4 +1343,51 @@ extern "C" int uor_gfx950_slice_gemm_i8(uint64_t m, uint64_t k, uint64_t n, cons
                                         uint64_t scratch_bytes, void *stream) {
     return uor_gfx950_slice_gemm_ex_i8(m, k, n, 1, a, a_len, k, b, b_len, n, 0, c, c_len, n,
                                        out_type, scratch, scratch_bytes, stream);
+}
+
+// ---------------------------------------------------- the no-alloc entry --
+//
+// For callers that cannot allocate device memory (code under graph capture,
+// serving loops, harnesses that forbid it): gemm_i8 with its scratch taken
+// from this file-scope array instead of an offer.  Each GPU holds its own
+// copy until the process ends; host code reaches it only through the
+// address hipGetSymbolAddress gives on that device (the array's name is a
+// host-side stand-in).  Every call on a GPU shares that GPU's copy, so calls
+// that overlap on one GPU race; what must start at zero (the split-K
+// partial sums) is cleared by the route itself, in stream order.
+static __device__ __align__(256) char scratch[UOR_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void *g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+}  // namespace
+
+extern "C" int uor_gfx950_gemm_i8_noalloc(const uor_view *a, const uor_view *b, const uor_view *c, int out_type,
+                                          int64_t alpha, int64_t beta, int encode, void *stream,
+                                          uor_route *route) {
+    route_set(route, UOR_ROUTE_NONE);
+    if (!valid_out_type(out_type) || !valid_encode(encode)) return UOR_INVALID_ARGUMENT;
+    Placed A, B, C;
+    int st = make_triple(a, 1, b, 1, c, out_type, &A, &B, &C);
+    if (st) return st;
+    if (C.rows == 0 || C.cols == 0) return UOR_OK;
+    // The scratch the fastest route takes (run_i8's split-K partial sums).
+    const uint64_t M = A.rows, K = A.cols, N = B.cols;
+    const uint64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+    const bool split = K > (uint64_t)KCHUNK || (t64 < 256 && K >= 8192);
+    if (split && splitk_bytes(M, N) > (uint64_t)UOR_NOALLOC_SCRATCH_BYTES) return UOR_SCRATCH_LIMIT;
+    int dev = 0;
+    UOR_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return UOR_INVALID_ARGUMENT;
+    std::call_once(g_scratch_once[dev], [dev] {
+        g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+    });
+    UOR_HIP(g_scratch_err[dev]);
+    void *const ptr = g_scratch_ptr[dev];
+    hipStream_t s = (hipStream_t)stream;
+    if (fits_fast(out_type, K, alpha, beta))
+        return run_i8<true>(A, B, C, out_type, alpha, beta, encode, ptr, UOR_NOALLOC_SCRATCH_BYTES, s, route);
+    return run_i8<false>(A, B, C, out_type, alpha, beta, encode, ptr, UOR_NOALLOC_SCRATCH_BYTES, s, route);
 }

@@ -20,7 +20,7 @@ LIB_PATH = pathlib.Path(os.environ.get("UOR_GFX950_LIB", HERE / "libuor_gfx950.s
 OUT = {"i8": 1, "i16": 2, "i32": 4, "i64": 8, "i128": 16}
 ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself", 3: "short_buffer",
-          4: "invalid_argument"}
+          4: "invalid_argument", 5: "scratch_limit"}
 ROUTES = {0: "none", 1: "epilogue_only", 2: "mfma_tile", 3: "mfma_splitk", 4: "mfma_wide",
           5: "collapsed",
           10: "lut4_dot4", 11: "lut4_mfma", 12: "lut4_prefill",
@@ -35,6 +35,7 @@ SYMBOLS = [
     "uor_gfx950_slice_gemm_ex_i8",
     "uor_gfx950_slice_gemm_i8",
     "uor_gfx950_suggested_scratch_i8",
+    "uor_gfx950_gemm_i8_noalloc",
     "uor_gfx950_gemm_int",
     "uor_gfx950_suggested_scratch_int",
     "uor_gfx950_gemm_lut4",
@@ -266,6 +267,27 @@ def slice_gemm_i8(m, k, n, a, b, c, out="i32", scratch=None, stream=None):
 
 def suggested_scratch_i8(m, k, n):
     return lib().uor_gfx950_suggested_scratch_i8(m, k, n)
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # UOR_NOALLOC_SCRATCH_BYTES
+
+
+def gemm_i8_noalloc(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+                    out="i32", alpha=1, beta=0, encode="nearest", stream=None):
+    """gemm_i8 with the library's static per-GPU scratch (no offer, no
+    allocation).  Returns (status, route dict)."""
+    ob = OUT[out]
+    av = view(a, *a_shape, *a_strides)
+    bv = view(b, *b_shape, *b_strides)
+    cv = view(c, *c_shape, *c_strides, elem=ob)
+    r = Route()
+    L = lib()
+    L.uor_gfx950_gemm_i8_noalloc.argtypes = [_PV, _PV, _PV, _i32, _i64, _i64, _i32, _vp, _PR]
+    L.uor_gfx950_gemm_i8_noalloc.restype = _i32
+    st = L.uor_gfx950_gemm_i8_noalloc(ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob,
+                                      int(alpha), int(beta), ENCODE[encode], _stream(stream),
+                                      ctypes.byref(r))
+    return st, r.as_dict()
 
 
 def gemm_int(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
