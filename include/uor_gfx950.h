@@ -186,8 +186,9 @@ int uor_gfx950_gemm_i8_noalloc(const uor_view *a, const uor_view *b, const uor_v
  * AccOf = i128 for i16/i32 and Limbs<3> for i64 (alphabet.rs:559-616,
  * acc.rs:215), Linear::finish and encode_i128_into / impl_encode_from_limbs
  * (epilogue.rs:67-95, acc.rs:128-150, 405-442).  The sum is exact at any
- * depth.  i64 elements: alpha = 1 and beta = 0 only (other scalars return
- * UOR_INVALID_ARGUMENT).  a, b: views of elem_bytes-byte integers; c: a view
+ * depth.  i64 elements scale and add in Limbs<3>'s 192-bit register, mod
+ * 2^192 (ScaleExact for Limbs, epilogue.rs:307-328).  a, b: views of
+ * elem_bytes-byte integers; c: a view
  * of `out_type` elements.  With an offer of uor_gfx950_suggested_scratch_int
  * bytes the int8 residue route runs; with none, a per-cell loop.
  */

@@ -221,6 +221,45 @@ static void l192_add_i128(l192 *x, i128 v) {
     x->w[2] = x->w[2] + ext + (uint64_t)(mid >> 64);
 }
 
+/* Two's complement negation over 192 bits (Limbs::neg, acc.rs:345-357). */
+static l192 l192_neg(l192 x) {
+    l192 r;
+    uint64_t carry = 1;
+    for (int i = 0; i < 3; i++) {
+        u128 t = (u128)(~x.w[i]) + carry;
+        r.w[i] = (uint64_t)t;
+        carry = (uint64_t)(t >> 64);
+    }
+    return r;
+}
+
+/* Limbs::combine (acc.rs:391-402): the sum mod 2^192. */
+static l192 l192_combine(l192 x, l192 y) {
+    l192 r;
+    uint64_t carry = 0;
+    for (int i = 0; i < 3; i++) {
+        u128 t = (u128)x.w[i] + y.w[i] + carry;
+        r.w[i] = (uint64_t)t;
+        carry = (uint64_t)(t >> 64);
+    }
+    return r;
+}
+
+/* ScaleExact for Limbs<L> (epilogue.rs:307-328): factor * x in the fixed
+ * 192-bit register, wrapping past it ("no growth", acc.rs:208-215).  The
+ * reference sums doublings of x (negated for a negative factor) over the bits
+ * of |factor|; that is the product mod 2^192, computed here directly. */
+static l192 l192_scale(l192 x, int64_t factor) {
+    const uint64_t f = factor < 0 ? (uint64_t)0 - (uint64_t)factor : (uint64_t)factor;
+    const u128 p0 = (u128)x.w[0] * f, p1 = (u128)x.w[1] * f;
+    l192 r;
+    r.w[0] = (uint64_t)p0;
+    const u128 s1 = (u128)(uint64_t)p1 + (uint64_t)(p0 >> 64);
+    r.w[1] = (uint64_t)s1;
+    r.w[2] = x.w[2] * f + (uint64_t)(p1 >> 64) + (uint64_t)(s1 >> 64);
+    return factor < 0 ? l192_neg(r) : r;
+}
+
 /* impl_encode_from_limbs (acc.rs:405-442). */
 static i128 encode_l192(const l192 *x, int out_bytes, int mode) {
     i128 low = (i128)(((u128)x->w[1] << 64) | x->w[0]);
@@ -253,8 +292,12 @@ static i128 encode_l192(const l192 *x, int out_bytes, int mode) {
  * i8/i16/i32, Limbs<3> for i64), then Linear::finish.  beta == 0 never reads C
  * (epilogue.rs:73-77, CS-04).
  *
- * elem_bytes in {1,2,4,8}; out_bytes in {1,2,4,8,16}.  For i64 elements only
- * alpha == 1, beta == 0 is restated (the CX-10 case).
+ * elem_bytes in {1,2,4,8}; out_bytes in {1,2,4,8,16}.  i64 elements: the
+ * Limbs<3> register (acc.rs:215), Linear::finish as scale_exact(alpha) +
+ * of_prior(C).scale_exact(beta), both mod 2^192 (epilogue.rs:80-95, 249-253,
+ * 307-328), then impl_encode_from_limbs.  Their modular lane (Wrapping into
+ * at most 64 bits, kernel.rs:371-398) is the same ring, so it gives the same
+ * bytes and is not restated separately.
  */
 int ora_gemm_int(int elem_bytes,
                  const void *a, uint64_t a_len, uint64_t a_rows, uint64_t a_cols, int64_t a_rs, int64_t a_cs,
@@ -269,7 +312,6 @@ int ora_gemm_int(int elem_bytes,
     view_t C = {c, c_len, c_rows, c_cols, c_rs, c_cs, 0};
     int st = make_triple(&A, &B, &C);
     if (st) return st;
-    if (elem_bytes == 8 && !(alpha == 1 && beta == 0)) return ORA_INVALID_ARGUMENT;
     uint64_t m = A.rows, k = A.cols, n = B.cols;
     for (uint64_t i = 0; i < m; i++) {
         for (uint64_t j = 0; j < n; j++) {
@@ -280,7 +322,13 @@ int ora_gemm_int(int elem_bytes,
                     i128 x = load_int(a, at(&A, i, p), 8), y = load_int(b, at(&B, p, j), 8);
                     l192_add_i128(&acc, x * y);
                 }
-                store_int(c, ci, out_bytes, encode_l192(&acc, out_bytes, mode));
+                l192 total = l192_scale(acc, alpha);
+                if (beta != 0) {
+                    l192 prior = {{0, 0, 0}};
+                    l192_add_i128(&prior, load_int(c, ci, out_bytes));
+                    total = l192_combine(total, l192_scale(prior, beta));
+                }
+                store_int(c, ci, out_bytes, encode_l192(&total, out_bytes, mode));
                 continue;
             }
             i128 acc = 0;

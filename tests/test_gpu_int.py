@@ -68,8 +68,8 @@ def run(oracle, uor, dev, eb, m, k, n, a_str=None, b_str=None, out="i64", alpha=
 @pytest.mark.parametrize("offer", [True, False])
 def test_shapes_against_oracle(oracle, uor, dev, eb, m, k, n, offer):
     """Full-range operands (extremes and zeros included); i64 output, with
-    alpha = 3, beta = -1 for i16/i32 elements (i64 elements: 1, 0)."""
-    alpha, beta = (1, 0) if eb == 8 else (3, -1)
+    alpha = 3, beta = -1."""
+    alpha, beta = 3, -1
     route = run(oracle, uor, dev, eb, m, k, n, alpha=alpha, beta=beta, offer=offer,
                 seed=eb * 1000 + m + k + n)
     want = ("int_limb" if eb < 8 else "int_crt") if offer else "int_direct"
@@ -83,7 +83,7 @@ def test_output_types_and_encodes(oracle, uor, dev, out, encode, eb):
     """Every output width under both integer encodes: sums far outside the
     narrow outputs saturate or wrap exactly as encode_i128_into /
     impl_encode_from_limbs do."""
-    scalars = [(1, 0)] if eb == 8 else [(1, 0), (3, -1), (1 << 40, -(1 << 35))]
+    scalars = [(1, 0), (3, -1), (1 << 40, -(1 << 35)), (-(1 << 63), (1 << 63) - 1)]
     for alpha, beta in scalars:
         run(oracle, uor, dev, eb, 9, 33, 21, out=out, alpha=alpha, beta=beta, encode=encode,
             seed=eb + 7)
@@ -159,13 +159,22 @@ def test_k_zero_and_empty(oracle, uor, dev):
     run(oracle, uor, dev, 8, 4, 5, 0)
 
 
-def test_i64_scalars_rejected(uor, dev):
-    """i64 elements take alpha = 1, beta = 0 only (Limbs<3> scaling is not
-    restated): anything else is an invalid argument, before any launch."""
-    a = torch.ones(4, dtype=torch.int64, device=dev)
-    c = torch.zeros(4, dtype=torch.int64, device=dev)
-    st, _ = uor.gemm_int(a, (2, 2), (2, 1), a, (2, 2), (2, 1), c, (2, 2), (2, 1), alpha=3)
-    assert uor.STATUS.get(st) == "invalid_argument"
+@pytest.mark.parametrize("offer", [True, False])
+def test_i64_register_wraps_mod_2_192(oracle, uor, dev, offer):
+    """Limbs<3>'s epilogue works in its fixed 192-bit register (epilogue.rs:
+    307-328, acc.rs:208-215): every element i64::MIN, k = 2^12, so the sum is
+    2^138; alpha = 2^54 gives 2^192 = 0, alpha = 2^53 gives 2^191 (the most
+    negative value: O::MIN), and beta * C adds mod 2^192 -- on the residue
+    route and on the per-cell loop, against the oracle."""
+    m, k, n = 2, 1 << 12, 3
+    a = np.full(m * k, np.iinfo(np.int64).min, np.int64)
+    b = np.full(k * n, np.iinfo(np.int64).min, np.int64)
+    for alpha, beta, out, encode in [(1 << 54, 0, "i64", "nearest"), (1 << 53, 0, "i32", "nearest"),
+                                     (1 << 53, -(1 << 63), "i64", "nearest"),
+                                     (1 << 52, 7, "i128", "nearest"), (3, -5, "i128", "wrapping"),
+                                     (-(1 << 63), (1 << 63) - 1, "i16", "wrapping")]:
+        run(oracle, uor, dev, 8, m, k, n, out=out, alpha=alpha, beta=beta, encode=encode,
+            offer=offer, a=a, b=b)
 
 
 def test_numpy_cx10_fixtures(uor, dev):

@@ -197,3 +197,126 @@ def test_wrapping_narrow_output_is_the_modular_lane(oracle):
     assert oracle.gemm_int(a, (1, k), (k, 1), a, (k, 1), (1, 1), c, (1, 1), (1, 1),
                            alpha=1, beta=1 << 62, encode="wrapping") == "ok"
     assert int(c[0]) == 8  # 8 + 3 * 2^62 mod 2^32
+
+
+# ---------------------------------------------------------------------------
+# Python-integer witnesses: the reference's integer epilogue written with
+# unbounded integers and explicit register widths, independent of the C
+# oracle's limb arithmetic.
+
+def _clamp(v, bits):
+    lo, hi = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+    return lo if v < lo else hi if v > hi else v
+
+
+def _wrap(v, bits):
+    v &= (1 << bits) - 1
+    return v - (1 << bits) if v >> (bits - 1) else v
+
+
+def py_finish(x, prior, alpha, beta, elem_bytes, out_bytes, mode):
+    """Linear::finish (epilogue.rs:80-95) and the one encode, for one cell.
+    i8/i16/i32 elements: the i128 register, saturating_mul then a wrapping
+    add (epilogue.rs:280-289, acc.rs:101-105); Wrapping into at most 32 bits
+    first reduces the sum to the Z/2^32 lane (kernel.rs:566-607).  i64
+    elements: Limbs<3>, every step mod 2^192 (epilogue.rs:307-328,
+    acc.rs:208-215).  Encode: Wrapping truncates, the other modes clamp
+    (acc.rs:128-150, 405-442)."""
+    ob = 8 * out_bytes
+    if elem_bytes == 8:
+        total = _wrap(x * alpha + (prior * beta if beta else 0), 192)
+    else:
+        if mode == "wrapping" and out_bytes <= 4:
+            x = _wrap(x, 32)
+        total = _clamp(x * alpha, 128)
+        if beta:
+            total = _wrap(total + _clamp(prior * beta, 128), 128)
+    return _wrap(total, ob) if mode == "wrapping" else _clamp(total, ob)
+
+
+def py_gemm(a, b, c0, alpha, beta, elem_bytes, out_bytes, mode):
+    m, k = a.shape
+    n = b.shape[1]
+    out = []
+    for i in range(m):
+        for j in range(n):
+            x = sum(int(a[i, p]) * int(b[p, j]) for p in range(k))
+            out.append(py_finish(x, int(c0[i * n + j]), alpha, beta, elem_bytes, out_bytes, mode))
+    return out
+
+
+def _c_ints(c, out_bytes):
+    if out_bytes == 16:
+        v = c.view(np.uint64).reshape(-1, 2)
+        return [_wrap(int(lo) | (int(hi) << 64), 128) for lo, hi in v]
+    return [int(x) for x in c]
+
+
+OUT_DT = {1: np.int8, 2: np.int16, 4: np.int32, 8: np.int64}
+
+
+@pytest.mark.parametrize("elem_bytes", [2, 4, 8])
+@pytest.mark.parametrize("out_bytes", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("mode", ["nearest", "saturating", "toward_zero", "wrapping"])
+def test_full_range_elements_against_python_ints(oracle, elem_bytes, out_bytes, mode):
+    """ora_gemm_int at i16/i32/i64 elements over full-range operands (the
+    extremes planted), every output width and encode, alpha/beta from 1/0 to
+    the i64 extremes, against the Python-integer restatement above."""
+    et = {2: np.int16, 4: np.int32, 8: np.int64}[elem_bytes]
+    info = np.iinfo(et)
+    rng = np.random.default_rng(1000 * elem_bytes + 10 * out_bytes + len(mode))
+    m, k, n = 3, 5, 4
+    a = rng.integers(info.min, info.max, (m, k), dtype=et, endpoint=True)
+    b = rng.integers(info.min, info.max, (k, n), dtype=et, endpoint=True)
+    a[0, :] = info.min
+    b[:, 0] = info.min
+    a[1, 0] = info.max
+    for alpha, beta in [(1, 0), (3, -1), (-(1 << 63), (1 << 63) - 1), ((1 << 62) + 3, -(1 << 40)),
+                        (0, 1), (-1, -(1 << 63))]:
+        if out_bytes == 16:
+            c0 = rng.integers(-(1 << 62), 1 << 62, 2 * m * n, dtype=np.int64)
+            c0.view(np.uint64)[1::2] = np.where(rng.random(m * n) < 0.5, 0, ~np.uint64(0))
+        else:
+            oi = np.iinfo(OUT_DT[out_bytes])
+            c0 = rng.integers(oi.min, oi.max, m * n, dtype=OUT_DT[out_bytes], endpoint=True)
+        prior = _c_ints(c0, out_bytes)
+        want = [py_finish(sum(int(a[i, p]) * int(b[p, j]) for p in range(k)), prior[i * n + j],
+                          alpha, beta, elem_bytes, out_bytes, mode)
+                for i in range(m) for j in range(n)]
+        c = c0.copy()
+        assert oracle.gemm_int(a.reshape(-1), (m, k), (k, 1), b.reshape(-1), (k, n), (n, 1), c,
+                               (m, n), (n, 1), alpha=alpha, beta=beta, encode=mode,
+                               out_bytes=out_bytes) == "ok"
+        assert _c_ints(c, out_bytes) == want, (alpha, beta)
+
+
+def test_i64_register_wraps_mod_2_192(oracle):
+    """Limbs<3> holds 192 bits and does not grow (acc.rs:208-215): with every
+    element i64::MIN and k = 2^20 the exact sum is 2^20 * 2^126 = 2^146, and
+    scale_exact(alpha) works in that register.  alpha = 2^46 gives 2^192,
+    which is 0; alpha = 2^45 gives 2^191, the register's most negative value,
+    so every clamping encode gives O::MIN; alpha = 2^44 gives 2^190 (O::MAX);
+    and beta * C adds mod 2^192 as well."""
+    k = 1 << 20
+    a = np.full(k, np.iinfo(np.int64).min, np.int64)
+    for alpha, out_dt, mode, want in [
+            (1 << 46, np.int64, "nearest", 0), (1 << 45, np.int64, "nearest", -(1 << 63)),
+            (1 << 45, np.int32, "saturating", -(1 << 31)), (1 << 44, np.int64, "toward_zero", (1 << 63) - 1),
+            (1 << 46, np.int16, "wrapping", 0), (3, np.int64, "wrapping", 0)]:
+        c = np.zeros(1, out_dt)
+        assert oracle.gemm_int(a, (1, k), (k, 1), a, (k, 1), (1, 1), c, (1, 1), (1, 1),
+                               alpha=alpha, encode=mode) == "ok"
+        assert int(c[0]) == want, (alpha, out_dt, mode)
+    # 2^191 + C * beta with C = i64::MIN, beta = i64::MIN: 2^191 + 2^126, still
+    # negative in the register; with beta = -i64::MAX instead: 2^191 - (2^63 - 1)
+    # * (-2^63) = 2^191 + 2^126 - 2^63.  Both clamp to i64::MIN.
+    for beta in (-(1 << 63), -((1 << 63) - 1)):
+        c = np.array([np.iinfo(np.int64).min], np.int64)
+        assert oracle.gemm_int(a, (1, k), (k, 1), a, (k, 1), (1, 1), c, (1, 1), (1, 1),
+                               alpha=1 << 45, beta=beta) == "ok"
+        assert int(c[0]) == -(1 << 63)
+    # i128 output, Wrapping: the register's low 128 bits of 2^146 * 3 are 0.
+    c = np.zeros(2, np.int64)
+    assert oracle.gemm_int(a, (1, k), (k, 1), a, (k, 1), (1, 1), c, (1, 1), (1, 1), alpha=3,
+                           encode="wrapping", out_bytes=16) == "ok"
+    assert c.tolist() == [0, 0]

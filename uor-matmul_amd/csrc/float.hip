@@ -1305,7 +1305,7 @@ struct IArgs {
     int64_t alpha, beta;
     int mode;
     int ob;     // output bytes
-    int limbs;  // 1: i64 elements (Limbs<3> accumulator; alpha = 1, beta = 0)
+    int limbs;  // 1: i64 elements (the Limbs<3> accumulator and epilogue)
 };
 
 template <int EB>
@@ -1321,6 +1321,40 @@ __device__ inline uint64_t mag64(int64_t v) { return v < 0 ? (uint64_t)0 - (uint
 struct W192 {
     uint64_t w[3];
 };
+
+// Limbs::neg (acc.rs:345-357), Limbs::combine (:391-402) and ScaleExact for
+// Limbs<L> (epilogue.rs:307-328): the register is 192 bits and does not grow,
+// so scaling by an i64 factor is the product mod 2^192.
+__device__ inline W192 w192_neg(const W192 &x) {
+    W192 r;
+    u128 t = (u128)(~x.w[0]) + 1;
+    r.w[0] = (uint64_t)t;
+    t = (u128)(~x.w[1]) + (uint64_t)(t >> 64);
+    r.w[1] = (uint64_t)t;
+    r.w[2] = ~x.w[2] + (uint64_t)(t >> 64);
+    return r;
+}
+
+__device__ inline W192 w192_combine(const W192 &x, const W192 &y) {
+    W192 r;
+    u128 t = (u128)x.w[0] + y.w[0];
+    r.w[0] = (uint64_t)t;
+    t = (u128)x.w[1] + y.w[1] + (uint64_t)(t >> 64);
+    r.w[1] = (uint64_t)t;
+    r.w[2] = x.w[2] + y.w[2] + (uint64_t)(t >> 64);
+    return r;
+}
+
+__device__ inline W192 w192_scale(const W192 &x, int64_t factor) {
+    const uint64_t f = factor < 0 ? (uint64_t)0 - (uint64_t)factor : (uint64_t)factor;
+    const u128 p0 = (u128)x.w[0] * f, p1 = (u128)x.w[1] * f;
+    W192 r;
+    r.w[0] = (uint64_t)p0;
+    const u128 s1 = (u128)(uint64_t)p1 + (uint64_t)(p0 >> 64);
+    r.w[1] = (uint64_t)s1;
+    r.w[2] = x.w[2] * f + (uint64_t)(p1 >> 64) + (uint64_t)(s1 >> 64);
+    return factor < 0 ? w192_neg(r) : r;
+}
 
 __device__ inline void w192_add(W192 &x, i128 v) {
     const u128 lo = (u128)x.w[0] + (uint64_t)(u128)v;
@@ -1476,14 +1510,25 @@ __device__ inline W192 int_direct_sum(const IArgs &F, uint64_t i, uint64_t j) {
 // Linear::finish and the one encode (epilogue.rs:67-95; acc.rs:128-150 for
 // i128, impl_encode_from_limbs acc.rs:405-442 for Limbs<3>).
 template <int OB>
-__device__ inline void int_finish(const IArgs &F, char *cp, const W192 &x) {
+__device__ inline void int_finish(const IArgs &F, char *cp, const W192 &sum) {
+    // i64 elements: Linear::finish in the Limbs<3> register, every step mod
+    // 2^192 (scale_exact(alpha) + of_prior(C).scale_exact(beta)).
+    W192 x = sum;
+    if (F.limbs && (F.alpha != 1 || F.beta != 0)) {
+        x = w192_scale(sum, F.alpha);
+        if (F.beta != 0) {
+            W192 prior{{0, 0, 0}};
+            w192_add(prior, load_out<OB>(cp));
+            x = w192_combine(x, w192_scale(prior, F.beta));
+        }
+    }
     i128 low = (i128)(((u128)x.w[1] << 64) | x.w[0]);
     // The public route's modular lane (kernel.rs:566-607, modular_spec and
     // modular_as_acc at :185-221, 250-279, 308-330): Wrapping into at most
     // 32 bits hands Linear::finish the sum in Z/2^32, sign-extended, so alpha
     // scales that lane and never saturates.  (i64 elements: Z/2^64 for
-    // outputs of at most 64 bits, which with alpha = 1, beta = 0 wraps to the
-    // same bytes as the exact value.)
+    // outputs of at most 64 bits, kernel.rs:371-398; every later step is mod
+    // 2^192, so that lane wraps to the same bytes as the exact value.)
     if (!F.limbs && OB <= 4 && F.mode == UOR_ENCODE_WRAPPING) low = (i128)(int32_t)(uint32_t)x.w[0];
     if (!F.limbs) {
         // i16 / i32 elements: |X| < 2^126, the i128 accumulator.
@@ -2063,9 +2108,6 @@ extern "C" int uor_gfx950_gemm_int(int elem_bytes, const uor_view *a, const uor_
     int st = make_triple(a, elem_bytes, b, elem_bytes, c, out_type, &A, &B, &C);
     if (st) return st;
     if (C.rows == 0 || C.cols == 0) return UOR_OK;
-    // Limbs<3>'s scale and prior rules are not restated: i64 elements take
-    // alpha = 1, beta = 0 only.
-    if (elem_bytes == 8 && !(alpha == 1 && beta == 0)) return UOR_INVALID_ARGUMENT;
     const uintptr_t oalign = (uintptr_t)(out_type < 8 ? out_type : 8) - 1;
     if ((((uintptr_t)A.base | (uintptr_t)B.base) & (uintptr_t)(elem_bytes - 1)) || ((uintptr_t)C.base & oalign))
         return UOR_INVALID_ARGUMENT;
