@@ -379,6 +379,22 @@ int uor_gfx950_slice_gemm_float_ex(int is_f64, uint64_t m, uint64_t k, uint64_t 
                                    uint64_t ldc, void *scratch, uint64_t scratch_bytes,
                                    void *stream);
 
+/* slice::gemm_float (slice.rs:405-421): gemm_float_ex(m,k,n,1,a,k,b,n,0,c,n).
+ *
+ * The reference's _full spellings take their working memory as several
+ * offers: gemm_float_ex_full / gemm_float_full (slice.rs:357-398, :428-465)
+ * as pa, pb, scaled, panels and accumulators, gemm_ex_full / gemm_full
+ * (slice.rs:221-279) as panels and accumulators.  Here they are the same call
+ * with ONE device offer: bind them to uor_gfx950_slice_gemm_float_ex /
+ * _float / uor_gfx950_slice_gemm_ex_i8 / _i8 with a single buffer of at most
+ * the offers' summed bytes.  As in the reference (CD-04, CD-10, CD-19) the
+ * bytes written to C are the same at every offer, empty included; the offer
+ * only selects the route, never the result. */
+int uor_gfx950_slice_gemm_float(int is_f64, uint64_t m, uint64_t k, uint64_t n,
+                                const void *a, uint64_t a_len, const void *b, uint64_t b_len,
+                                void *c, uint64_t c_len, void *scratch, uint64_t scratch_bytes,
+                                void *stream);
+
 /*
  * raw::sgemm / raw::dgemm (crates/uor-matmul/src/raw.rs:45-90, raw_gemm
  * :98-158): matrixmultiply's signature.  a, b, c point at element (0,0);
@@ -485,6 +501,57 @@ int uor_gfx950_gemm_trop_i8_selected(const uor_view *a, const uor_view *b,
                                      int mechanism, void *scratch,
                                      uint64_t scratch_bytes, void *stream,
                                      uor_route *route);
+
+/* ========================================= partition of the output (S12) */
+
+/* One independently computable block of C (partition.rs:16-27 Tile). */
+typedef struct uor_tile {
+    uint64_t row, col;   /* first row and column of C */
+    uint64_t rows, cols; /* extent, clipped at C's last row and column */
+} uor_tile;
+
+/* Partition::new + len (crates/uor-matmul-gemm/src/partition.rs:44-66): the
+ * number of tiles of at most tile_rows x tile_cols covering an m x n output;
+ * a zero tile extent means the whole extent.  0 exactly when m or n is 0. */
+uint64_t uor_gfx950_partition_len(uint64_t m, uint64_t n, uint64_t tile_rows,
+                                  uint64_t tile_cols);
+
+/* Partition::tile (partition.rs:83-98): tile `index` in the stable row-major
+ * tile order.  Returns 1 and fills *out, or 0 (None) when index >= len. */
+int uor_gfx950_partition_tile(uint64_t m, uint64_t n, uint64_t tile_rows,
+                              uint64_t tile_cols, uint64_t index, uor_tile *out);
+
+/* MatView::subview (crates/uor-matmul-core/src/layout.rs:633-646): the
+ * rows x cols block of *v at (i, j), as a view of its own into the same
+ * buffer (same strides; data and len narrowed to the block's window).
+ * UOR_INVALID_ARGUMENT where the reference returns None (the block reaches
+ * outside the view), UOR_SHORT_BUFFER when *v itself does not fit. */
+int uor_gfx950_subview(const uor_view *v, int elem_bytes, uint64_t i, uint64_t j,
+                       uint64_t rows, uint64_t cols, uor_view *out);
+
+/*
+ * The partition driven on streams (the caller-side executor the reference
+ * leaves to rayon and the like, partition.rs:1-11): tile t runs as its own
+ * uor_gfx950_gemm_i8 / _gemm_float over the sub-views A[row.., :],
+ * B[:, col..], C[row.., col..] on streams[t % nstreams] (nstreams 0: the null
+ * stream).  The offer is split into nstreams equal 256-aligned shares, one
+ * per stream.  The bytes of C equal the single call's for every tile shape and
+ * stream count (CD-02): the tiles are disjoint and each cell is one exact sum.
+ * The whole call is checked as the single call checks it before any tile is
+ * enqueued; *tiles_run (may be NULL) counts the tiles enqueued.  The caller
+ * orders the streams after its own work on A, B and C and joins them after;
+ * streams must have the default priority.
+ */
+int uor_gfx950_gemm_i8_tiled(const uor_view *a, const uor_view *b, const uor_view *c,
+                             int out_type, int64_t alpha, int64_t beta, int encode,
+                             uint64_t tile_rows, uint64_t tile_cols, void *const *streams,
+                             uint32_t nstreams, void *scratch, uint64_t scratch_bytes,
+                             uint64_t *tiles_run);
+int uor_gfx950_gemm_float_tiled(int is_f64, const uor_view *a, const uor_view *b,
+                                const uor_view *c, int64_t alpha, int64_t beta, int encode,
+                                uint64_t tile_rows, uint64_t tile_cols, void *const *streams,
+                                uint32_t nstreams, void *scratch, uint64_t scratch_bytes,
+                                uint64_t *tiles_run);
 
 #ifdef __cplusplus
 }

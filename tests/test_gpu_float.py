@@ -220,6 +220,30 @@ def test_dgemm_and_slice_faces(oracle, uor, dev):
         assert np.array_equal(bits(gc.cpu().numpy()), bits(want))
 
 
+@pytest.mark.parametrize("is64", [False, True])
+def test_slice_gemm_float_every_offer(oracle, uor, dev, is64):
+    """slice::gemm_float (slice.rs:405-421) against the oracle at alpha 1,
+    beta 0, and the same bytes at every offer: none, a few bytes, an eighth of
+    the suggestion, the suggestion and more (CD-19: the _full spellings' offers
+    fold into this one buffer and never change the result)."""
+    m, k, n = 37, 300, 29
+    a, b = gen.corpus_operands((m, k, n, "FewGrades", 5), is64)
+    want = np.zeros(m * n, a.dtype)
+    oracle.gemm_float(a, (m, k), (k, 1), b, (k, n), (n, 1), want, (m, n), (n, 1))
+    ga, gb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    full = uor.suggested_scratch_float(is64, m, k, n)
+    assert full > 0
+    for nbytes in (0, 8, full // 8, full, full + 4096):
+        scratch = torch.empty(nbytes + 64, dtype=torch.uint8, device=dev)[64:] if nbytes else None
+        gc = torch.full((m * n,), 7.0, dtype=ga.dtype, device=dev)
+        assert uor.slice_gemm_float(m, k, n, ga, gb, gc, scratch=scratch) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(gc.cpu().numpy()), bits(want)), nbytes
+    # A C slice shorter than m * n is refused before anything runs.
+    short = torch.zeros(m * n - 1, dtype=ga.dtype, device=dev)
+    assert uor.STATUS[uor.slice_gemm_float(m, k, n, ga, gb, short)] == "short_buffer"
+
+
 @pytest.mark.parametrize("offer", OFFERS)
 @pytest.mark.parametrize("is64,m,k,n", [(False, 48, 4096, 40), (True, 24, 2048, 20)])
 def test_config4_distribution_reduced(oracle, uor, dev, is64, m, k, n, offer):

@@ -1776,6 +1776,16 @@ extern "C" int uor_gfx950_slice_gemm_float_ex(int is_f64, uint64_t m, uint64_t k
                                  scratch_bytes, stream, nullptr);
 }
 
+// slice.rs:405-421 gemm_float: gemm_float_ex at alpha 1, beta 0, lda = k,
+// ldb = n, ldc = n.
+extern "C" int uor_gfx950_slice_gemm_float(int is_f64, uint64_t m, uint64_t k, uint64_t n,
+                                           const void *a, uint64_t a_len, const void *b,
+                                           uint64_t b_len, void *c, uint64_t c_len, void *scratch,
+                                           uint64_t scratch_bytes, void *stream) {
+    return uor_gfx950_slice_gemm_float_ex(is_f64, m, k, n, 1, a, a_len, k, b, b_len, n, 0, c,
+                                          c_len, n, scratch, scratch_bytes, stream);
+}
+
 // raw.rs low() / span(): the lowest offset a view reaches and its extent, or
 // false when they overflow.
 static bool raw_window(uint64_t rows, uint64_t cols, int64_t rs, int64_t cs, int64_t *low,

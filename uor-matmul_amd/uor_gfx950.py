@@ -49,6 +49,7 @@ SYMBOLS = [
     "uor_gfx950_manifest_json",
     "uor_gfx950_gemm_float",
     "uor_gfx950_slice_gemm_float_ex",
+    "uor_gfx950_slice_gemm_float",
     "uor_gfx950_sgemm",
     "uor_gfx950_dgemm",
     "uor_gfx950_suggested_scratch_float",
@@ -56,12 +57,25 @@ SYMBOLS = [
     "uor_gfx950_gemm_trop_i8_selected",
     "uor_gfx950_gemm_collapsed_i8",
     "uor_gfx950_suggested_scratch_collapse",
+    "uor_gfx950_partition_len",
+    "uor_gfx950_partition_tile",
+    "uor_gfx950_subview",
+    "uor_gfx950_gemm_i8_tiled",
+    "uor_gfx950_gemm_float_tiled",
 ]
 
 
 class View(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("len", ctypes.c_uint64), ("rows", ctypes.c_uint64),
                 ("cols", ctypes.c_uint64), ("rs", ctypes.c_int64), ("cs", ctypes.c_int64)]
+
+
+class Tile(ctypes.Structure):
+    _fields_ = [("row", ctypes.c_uint64), ("col", ctypes.c_uint64), ("rows", ctypes.c_uint64),
+                ("cols", ctypes.c_uint64)]
+
+    def as_tuple(self):
+        return (self.row, self.col, self.rows, self.cols)
 
 
 class Codec(ctypes.Structure):
@@ -122,6 +136,23 @@ def lib():
         L.uor_gfx950_slice_gemm_i8.restype = _i32
         L.uor_gfx950_suggested_scratch_i8.argtypes = [_u64, _u64, _u64]
         L.uor_gfx950_suggested_scratch_i8.restype = _u64
+        if hasattr(L, "uor_gfx950_partition_len"):
+            L.uor_gfx950_partition_len.argtypes = [_u64, _u64, _u64, _u64]
+            L.uor_gfx950_partition_len.restype = _u64
+            L.uor_gfx950_partition_tile.argtypes = [_u64, _u64, _u64, _u64, _u64,
+                                                    ctypes.POINTER(Tile)]
+            L.uor_gfx950_partition_tile.restype = _i32
+            L.uor_gfx950_subview.argtypes = [_PV, _i32, _u64, _u64, _u64, _u64, _PV]
+            L.uor_gfx950_subview.restype = _i32
+            L.uor_gfx950_gemm_i8_tiled.argtypes = [_PV, _PV, _PV, _i32, _i64, _i64, _i32, _u64,
+                                                   _u64, ctypes.POINTER(_vp), ctypes.c_uint32,
+                                                   _vp, _u64, ctypes.POINTER(_u64)]
+            L.uor_gfx950_gemm_i8_tiled.restype = _i32
+            L.uor_gfx950_gemm_float_tiled.argtypes = [_i32, _PV, _PV, _PV, _i64, _i64, _i32,
+                                                      _u64, _u64, ctypes.POINTER(_vp),
+                                                      ctypes.c_uint32, _vp, _u64,
+                                                      ctypes.POINTER(_u64)]
+            L.uor_gfx950_gemm_float_tiled.restype = _i32
         if hasattr(L, "uor_gfx950_gemm_int"):
             L.uor_gfx950_gemm_int.argtypes = [_i32, _PV, _PV, _PV, _i32, _i64, _i64, _i32, _vp,
                                               _u64, _vp, _PR]
@@ -171,6 +202,9 @@ def lib():
                                                          _u64, _vp, _u64, _u64, _i64, _vp, _u64,
                                                          _u64, _vp, _u64, _vp]
             L.uor_gfx950_slice_gemm_float_ex.restype = _i32
+            L.uor_gfx950_slice_gemm_float.argtypes = [_i32, _u64, _u64, _u64, _vp, _u64, _vp,
+                                                      _u64, _vp, _u64, _vp, _u64, _vp]
+            L.uor_gfx950_slice_gemm_float.restype = _i32
             for name in ("uor_gfx950_sgemm", "uor_gfx950_dgemm"):
                 f = getattr(L, name)
                 f.argtypes = [_u64, _u64, _u64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
@@ -246,6 +280,75 @@ def gemm_i8(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
                                   int(alpha), int(beta), ENCODE[encode], _ptr(scratch),
                                   _nbytes(scratch), _stream(stream), ctypes.byref(r))
     return st, r.as_dict()
+
+
+def partition_len(m, n, tile_rows, tile_cols):
+    """Partition::new(..).len(): tiles of at most tile_rows x tile_cols (0 = whole extent)."""
+    return lib().uor_gfx950_partition_len(m, n, tile_rows, tile_cols)
+
+
+def partition_tile(m, n, tile_rows, tile_cols, index):
+    """Partition::tile: (row, col, rows, cols) of tile `index`, or None past the end."""
+    t = Tile()
+    if not lib().uor_gfx950_partition_tile(m, n, tile_rows, tile_cols, index, ctypes.byref(t)):
+        return None
+    return t.as_tuple()
+
+
+def partition(m, n, tile_rows, tile_cols):
+    """The Partition iterator: every tile in the stable order."""
+    for i in range(partition_len(m, n, tile_rows, tile_cols)):
+        yield partition_tile(m, n, tile_rows, tile_cols, i)
+
+
+def subview(v, elem, i, j, rows, cols):
+    """MatView::subview over a View: (status, View)."""
+    out = View()
+    st = lib().uor_gfx950_subview(ctypes.byref(v), elem, i, j, rows, cols, ctypes.byref(out))
+    return st, out
+
+
+def _streams(streams):
+    if not streams:
+        return None, 0
+    arr = (_vp * len(streams))(*[s.cuda_stream if hasattr(s, "cuda_stream") else s
+                                 for s in streams])
+    return arr, len(streams)
+
+
+def gemm_i8_tiled(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+                  tile_rows, tile_cols, streams=(), out="i32", alpha=1, beta=0,
+                  encode="nearest", scratch=None):
+    """The partition run on streams (tile t on streams[t % len]): (status, tiles enqueued)."""
+    ob = OUT[out]
+    av = view(a, *a_shape, *a_strides)
+    bv = view(b, *b_shape, *b_strides)
+    cv = view(c, *c_shape, *c_strides, elem=ob)
+    arr, ns = _streams(streams)
+    ran = _u64(0)
+    st = lib().uor_gfx950_gemm_i8_tiled(ctypes.byref(av), ctypes.byref(bv), ctypes.byref(cv), ob,
+                                        int(alpha), int(beta), ENCODE[encode], tile_rows,
+                                        tile_cols, arr, ns, _ptr(scratch), _nbytes(scratch),
+                                        ctypes.byref(ran))
+    return st, ran.value
+
+
+def gemm_float_tiled(a, a_shape, a_strides, b, b_shape, b_strides, c, c_shape, c_strides,
+                     tile_rows, tile_cols, streams=(), alpha=1, beta=0, encode="nearest",
+                     scratch=None):
+    import torch
+    is64 = int(a.dtype == torch.float64)
+    es = 8 if is64 else 4
+    av = view(a, *a_shape, *a_strides, elem=es)
+    bv = view(b, *b_shape, *b_strides, elem=es)
+    cv = view(c, *c_shape, *c_strides, elem=es)
+    arr, ns = _streams(streams)
+    ran = _u64(0)
+    st = lib().uor_gfx950_gemm_float_tiled(is64, ctypes.byref(av), ctypes.byref(bv),
+                                           ctypes.byref(cv), int(alpha), int(beta),
+                                           ENCODE[encode], tile_rows, tile_cols, arr, ns,
+                                           _ptr(scratch), _nbytes(scratch), ctypes.byref(ran))
+    return st, ran.value
 
 
 def slice_gemm_ex_i8(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, out="i32", scratch=None,
@@ -352,6 +455,17 @@ def slice_gemm_float_ex(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, scratch=No
     return lib().uor_gfx950_slice_gemm_float_ex(
         is64, m, k, n, int(alpha), _ptr(a), _len(a, es), lda, _ptr(b), _len(b, es), ldb,
         int(beta), _ptr(c), _len(c, es), ldc, _ptr(scratch), _nbytes(scratch), _stream(stream))
+
+
+def slice_gemm_float(m, k, n, a, b, c, scratch=None, stream=None):
+    """slice::gemm_float: contiguous row-major, alpha 1, beta 0."""
+    import torch
+    is64 = int(a.dtype == torch.float64)
+    es = 8 if is64 else 4
+    a, b, c = _dev(a), _dev(b), _dev(c)
+    return lib().uor_gfx950_slice_gemm_float(
+        is64, m, k, n, _ptr(a), _len(a, es), _ptr(b), _len(b, es), _ptr(c), _len(c, es),
+        _ptr(scratch), _nbytes(scratch), _stream(stream))
 
 
 def raw_gemm(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, a_off=0, b_off=0,
