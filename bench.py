@@ -382,7 +382,7 @@ def bench_collapse(args, torch, uor, gen):
     N, D = 8192, 512
     dev = torch.device("cuda:0")
     base = torch.from_numpy(gen.i8_full(D * N, 31)).to(dev).view(D, N)
-    pick = torch.from_numpy((gen.lanes_draws(N, 32) % np.uint64(D)).astype(np.int64)).to(dev)
+    pick = torch.from_numpy((gen.draws(N, 32) % np.uint64(D)).astype(np.int64)).to(dev)
     pick[:D] = torch.arange(D, device=dev)
     a = base[pick].contiguous().view(-1)
     b = torch.from_numpy(gen.i8_full(N * N, 33)).to(dev)
@@ -437,7 +437,7 @@ def bench_trop(args, torch, uor, gen):
 
     def recs(salt):
         v = gen.i8_full(N * N, salt)
-        f = (gen.lanes_draws(N * N, 100 + salt) % np.uint64(20)) != 0
+        f = (gen.draws(N * N, 100 + salt) % np.uint64(20)) != 0
         r = np.zeros(N * N, rec)
         r["value"] = np.where(f, v, 0)
         r["finite"] = f
@@ -732,8 +732,8 @@ def bench_config1(args, torch, uor, gen):
     offer; launch-bound at this size.  Checked in float64 (exact here)."""
     n = 1024
     dev = torch.device("cuda:0")
-    a = gen.i8_full(n * n, 1, exact_sequence=True)
-    b = gen.i8_full(n * n, 2, exact_sequence=True)
+    a = gen.i8_full(n * n, 1)
+    b = gen.i8_full(n * n, 2)
     ga, gb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
     gc = torch.zeros(n * n, dtype=torch.int32, device=dev)
     sc = torch.empty(uor.suggested_scratch_i8(n, n, n), dtype=torch.uint8, device=dev)

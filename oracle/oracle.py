@@ -19,7 +19,10 @@ import subprocess
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
-LIB = HERE / "liboracle.so"
+# UOR_ORACLE_VARIANT=asan selects the AddressSanitizer/UBSan builds that
+# `make -C oracle asan` makes and runs the CPU suite against.
+_VARIANT = "_asan" if os.environ.get("UOR_ORACLE_VARIANT") == "asan" else ""
+LIB = HERE / f"liboracle{_VARIANT}.so"
 
 ENCODE = {"nearest": 0, "toward_zero": 1, "saturating": 2, "wrapping": 3}
 STATUS = {0: "ok", 1: "nonconformant", 2: "output_aliases_itself",
@@ -32,7 +35,8 @@ _lib = None
 
 
 def build() -> None:
-    subprocess.run(["make", "-s", "-C", str(HERE), "-B", "all"], check=True)
+    target = "asan-libs" if _VARIANT else "all"
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B", target], check=True)
 
 
 def lib():
@@ -173,7 +177,7 @@ def trop_bytes(rec):
 
 
 # ------------------------------------------------------------ CPU baseline
-FAST = HERE / "libfastroute.so"
+FAST = HERE / f"libfastroute{_VARIANT}.so"
 _fast = None
 
 

@@ -2,9 +2,9 @@
 
 `fill` is the reference corpus generator: xorshift64 (13, 7, 17) seeded with
 0x243F6A8885A308D3 ^ salt, one draw per element, value (s >> 33)
-(crates/uor-matmul-validate/tests/massive.rs:42-53), vectorised over
-independent lanes for large sizes (each lane is its own xorshift stream
-seeded from the salt and the lane index) so multi-GiB fills take seconds.
+(crates/uor-matmul-validate/tests/massive.rs:42-53).  `draws` produces that
+exact sequence for any length, split over parallel lanes whose start states
+come from GF(2) jump-ahead, so multi-GiB fills take seconds.
 """
 from __future__ import annotations
 
@@ -26,32 +26,71 @@ def xorshift_draws(n: int, salt: int) -> np.ndarray:
     return out
 
 
-def lanes_draws(n: int, salt: int, lanes: int = 1 << 16) -> np.ndarray:
-    """n draws from `lanes` independent xorshift streams (round robin)."""
+def _step_columns() -> np.ndarray:
+    """One xorshift step is linear over GF(2)^64: column b is the image of bit b."""
+    cols = []
+    for b in range(64):
+        s = 1 << b
+        s ^= (s << 13) & M64
+        s ^= s >> 7
+        s ^= (s << 17) & M64
+        cols.append(s)
+    return np.array(cols, dtype=np.uint64)
+
+
+def _apply(cols: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """The GF(2) matrix with these 64 columns times every state in v."""
+    out = np.zeros_like(v)
+    one = np.uint64(1)
+    for b in range(64):
+        out ^= cols[b] * ((v >> np.uint64(b)) & one)
+    return out
+
+
+def _power(cols: np.ndarray, e: int) -> np.ndarray:
+    """The columns of the e-th power (e >= 0) by repeated squaring."""
+    result = np.array([1 << b for b in range(64)], dtype=np.uint64)
+    base = cols.copy()
+    while e:
+        if e & 1:
+            result = _apply(base, result)
+        base = _apply(base, base)
+        e >>= 1
+    return result
+
+
+def draws(n: int, salt: int, lanes: int = 1 << 16) -> np.ndarray:
+    """xorshift_draws(n, salt) exactly, computed in parallel: lane i starts
+    at state M^(i*L) s0 (M the step, L = ceil(n / lanes), the start states by
+    GF(2) jump-ahead) and produces draws i*L .. i*L + L - 1."""
+    if n <= 0:
+        return np.empty(0, dtype=np.uint64)
     lanes = max(1, min(lanes, n))
-    idx = np.arange(lanes, dtype=np.uint64)
-    s = (np.uint64(SEED) ^ np.uint64(salt)) ^ (idx * np.uint64(0x9E3779B97F4A7C15))
-    s[s == 0] = np.uint64(1)
-    rounds = (n + lanes - 1) // lanes
-    out = np.empty(rounds * lanes, dtype=np.uint64)
+    L = (n + lanes - 1) // lanes
+    jump = _power(_step_columns(), L)
+    starts = np.array([(SEED ^ salt) & M64], dtype=np.uint64)
+    while starts.size < lanes:
+        starts = np.concatenate([starts, _apply(jump, starts)])
+        jump = _apply(jump, jump)
+    s = starts[:lanes].copy()
+    out = np.empty((L, lanes), dtype=np.uint64)
     sh13, sh7, sh17, sh33 = np.uint64(13), np.uint64(7), np.uint64(17), np.uint64(33)
-    for r in range(rounds):
+    for r in range(L):
         s ^= s << sh13
         s ^= s >> sh7
         s ^= s << sh17
-        out[r * lanes:(r + 1) * lanes] = s >> sh33
-    return out[:n]
+        out[r] = s >> sh33
+    return np.ascontiguousarray(out.T).reshape(-1)[:n]
 
 
-def i8_full(n: int, salt: int, exact_sequence: bool = False) -> np.ndarray:
+def i8_full(n: int, salt: int) -> np.ndarray:
     """Uniform over all 256 i8 values: (s >> 33) as u8 as i8."""
-    d = xorshift_draws(n, salt) if exact_sequence else lanes_draws(n, salt)
-    return (d & np.uint64(0xFF)).astype(np.uint8).view(np.int8)
+    return (draws(n, salt) & np.uint64(0xFF)).astype(np.uint8).view(np.int8)
 
 
 def i32_pm2_20(n: int, salt: int) -> np.ndarray:
     """Uniform i32 in [-2^20, 2^20]: (s >> 33) mod (2^21 + 1) - 2^20."""
-    d = lanes_draws(n, salt)
+    d = draws(n, salt)
     return ((d % np.uint64((1 << 21) + 1)).astype(np.int64) - (1 << 20)).astype(np.int32)
 
 
@@ -62,8 +101,8 @@ def float_config4(rows: int, cols: int, is64: bool, salt: int) -> np.ndarray:
     x 2^e, e uniform over [-40, 40] (f32) or [-300, 300] (f64), with 1% exact
     zeros.  Built from IEEE fields so no host rounding is involved."""
     n = rows * cols
-    d1 = lanes_draws(n, salt)
-    d2 = lanes_draws(n, salt + 0x5151)
+    d1 = draws(n, salt)
+    d2 = draws(n, salt + 0x5151)
     span = 300 if is64 else 40
     mant_bits, bias = (52, 1023) if is64 else (23, 127)
     e = (d1 % np.uint64(2 * span + 1)).astype(np.int64) - span
@@ -83,7 +122,7 @@ def cancel_pairs(a: np.ndarray, b: np.ndarray, salt: int, frac: float = 0.01):
     equals row p, so A[i,p]*B[p,j] + A[i,q]*B[q,j] = 0 for every i, j."""
     k = a.shape[1]
     npairs = max(1, int(k * frac)) if k >= 2 else 0
-    perm = np.argsort(lanes_draws(k, salt), kind="stable")
+    perm = np.argsort(draws(k, salt), kind="stable")
     for t in range(npairs):
         p, q = int(perm[2 * t]), int(perm[2 * t + 1])
         a[:, q] = -a[:, p]

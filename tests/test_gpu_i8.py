@@ -226,8 +226,8 @@ def test_config1_slice_gemm_1024(uor, dev):
     """configs[0]: slice::gemm i8 -> i32, 1024^3, xorshift fill (salts 1, 2),
     suggested scratch offer; the reference's exact generator sequence."""
     n = 1024
-    a = gen.i8_full(n * n, 1, exact_sequence=True)
-    b = gen.i8_full(n * n, 2, exact_sequence=True)
+    a = gen.i8_full(n * n, 1)
+    b = gen.i8_full(n * n, 2)
     want = (a.reshape(n, n).astype(np.float64) @ b.reshape(n, n).astype(np.float64)).astype(np.int32)
     scratch = torch.empty(uor.suggested_scratch_i8(n, n, n), dtype=torch.uint8, device=dev)
     gc = torch.full((n * n,), 0x7B7B7B7B, dtype=torch.int32, device=dev)

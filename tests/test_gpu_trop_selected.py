@@ -202,8 +202,8 @@ def test_config5_4096(oracle, uor, dev):
     N = 4096
     va = gen.i8_full(N * N, 11).astype(np.int64)
     vb = gen.i8_full(N * N, 12).astype(np.int64)
-    fa = (gen.lanes_draws(N * N, 111) % np.uint64(20)) != 0
-    fb = (gen.lanes_draws(N * N, 112) % np.uint64(20)) != 0
+    fa = (gen.draws(N * N, 111) % np.uint64(20)) != 0
+    fb = (gen.draws(N * N, 112) % np.uint64(20)) != 0
 
     def recs(v, f):
         r = np.zeros(v.size, REC[1])
