@@ -48,6 +48,9 @@ def log(msg):
 
 
 SETTLE_S = 0.3  # untimed running before each timed region, so clocks reach steady state
+# Host copies of the secondary configs' inputs and of the GPU's outputs, kept
+# for the CPU-baseline leg, which checks every CPU result against them.
+CPU_INPUTS = {}
 
 
 def settle(torch, step, seconds=None):
@@ -270,6 +273,13 @@ def bench_lut4(args, torch, uor, gen, ms_list=(1, 8, 32)):
         ms = s0.elapsed_time(s1) / steps
         nbytes = n * k // 2 + m * k + 4 * m * n + (n // group) * 16
         gbs = nbytes / (ms * 1e-3) / 1e9
+        if "cpu" in args.parts:
+            step(0)
+            torch.cuda.synchronize()
+            lut = CPU_INPUTS.setdefault("lut", {"k": k, "n": n, "group": group,
+                                               "codes": codes[0].cpu().numpy(),
+                                               "books": books.cpu().numpy(), "runs": {}})
+            lut["runs"][m] = (a.cpu().numpy(), c.cpu().numpy())
         out.append({"m": m, "k": k, "n": n, "group": group, "ms_per_call": round(ms, 5),
                     "GB_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                     "TOPS": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
@@ -477,6 +487,9 @@ def bench_trop(args, torch, uor, gen):
 
     terms = float(N) ** 3
     ms = timed(plain)
+    if "cpu" in args.parts:
+        CPU_INPUTS["trop"] = {"N": N, "a": a.cpu().numpy(), "b": b.cpu().numpy(),
+                              "c": c.cpu().numpy()}
     rate = terms / (ms * 1e-3)
     ms_sel = timed(selected)
     rate_sel = terms / (ms_sel * 1e-3)
@@ -534,13 +547,12 @@ def bench_float(args, torch, uor, gen):
 
         step(sc)
         torch.cuda.synchronize()
-        if not is64:
-            settle(torch, lambda: step(sc))
+        settle(torch, lambda: step(sc))
         plan = None
         if sc is not None:
             off = (-sc.data_ptr()) % 256
             plan = sc[off:off + 12].cpu().view(torch.int32).tolist()
-        steps = max(1, min(args.steps, 20)) if not is64 else 1
+        steps = max(1, min(args.steps, 20)) if not is64 else max(3, min(args.steps, 5))
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s0.record(stream)
         for _ in range(steps):
@@ -549,6 +561,10 @@ def bench_float(args, torch, uor, gen):
         torch.cuda.synchronize()
         ms = s0.elapsed_time(s1) / steps
         fast = c.clone()
+        if "cpu" in args.parts:
+            CPU_INPUTS.setdefault("float", []).append(
+                {"is64": is64, "N": N, "a": ga.cpu().numpy(), "b": gb.cpu().numpy(),
+                 "c": fast[:64 * N].cpu().numpy()})
         kind = route.get("kind")
         parity = None
         if sc is not None:
@@ -764,17 +780,47 @@ def bench_config1(args, torch, uor, gen):
             "TOPS": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1), "parity": parity}
 
 
+def cpu_threads():
+    """The worker count for the CPU leg: every core this process may run on,
+    at most 16 (one GPU's share of the GPU box's cores)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return max(1, min(usable, 16)), usable
+
+
+def cpu_host():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads, usable = cpu_threads()
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "usable_cpus": usable,
+            "threads_used": threads}
+
+
+def median_time(fn, runs=5):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
 def cpu_baseline_i8(host, oracle):
     """The reference's packed route restated (oracle/fastroute.cpp) on a row
-    slab of the same 8192^3 problem, all usable host cores."""
+    slab of the same 8192^3 problem, all usable host cores, then one core."""
     import numpy as np
     a, b, c0 = host
     N, LD = 8192, 8256
-    try:
-        threads = len(os.sched_getaffinity(0))
-    except AttributeError:
-        threads = os.cpu_count() or 1
-    threads = max(1, min(threads, 16))
+    threads, _ = cpu_threads()
     c = c0.copy()
     rows = 16
     t0 = time.perf_counter()
@@ -788,6 +834,12 @@ def cpu_baseline_i8(host, oracle):
                             threads=threads)
     dt = time.perf_counter() - t0
     ops = 2.0 * rows2 * N * N
+    # One core: an 8-row slab (one A panel against all of B).
+    c1 = c0.copy()
+    t0 = time.perf_counter()
+    oracle.fast_gemm_i8_i32(N, N, N, 3, a, LD, b, LD, -1, c1, LD, row0=0, rows=8, threads=1)
+    dt1 = time.perf_counter() - t0
+    same = bool(np.array_equal(c1[:8 * LD], c[:8 * LD]))
     vnni = bool(oracle.fast().fr_has_vnni())
     return {
         "value": round(ops / dt / 1e12, 4),
@@ -797,7 +849,106 @@ def cpu_baseline_i8(host, oracle):
         "sample": f"rows 0..{rows2} of the 8192^3 gemm_ex (alpha=3, beta=-1), "
                   f"{dt:.1f} s on {threads} threads, {'AVX-512 VNNI dpbusd' if vnni else 'AVX2'} "
                   "8x16 tile; rows are independent so TOPS scale to the full problem",
+        "one_core": {"value": round(2.0 * 8 * N * N / dt1 / 1e12, 4), "unit": "TOPS",
+                     "sample": f"rows 0..8, {dt1:.2f} s", "same_bytes_as_all_cores": same},
+        "host": cpu_host(),
     }
+
+
+def cpu_baselines_secondary(oracle):
+    """CPU restatements for the secondary configs, each checked byte for byte
+    against the GPU's output on the same inputs:
+      LUT decode: tabulation and decode-then-dense, one call per
+        codebook group (224 calls), all groups on all cores, the first 28
+        groups on one core (extrapolated x 8);
+      max-plus: the AVX2_TROP_I16 tile, all 4096 rows on all
+        cores, 256 rows on one core (extrapolated);
+      exact float: the oracle's per-product exact register on a
+        64-row slab on all cores (extrapolated to the full problem), 8 rows on
+        one core."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    threads, _ = cpu_threads()
+    out = {"host": cpu_host()}
+    lut = CPU_INPUTS.get("lut")
+    if lut:
+        k, n, group = lut["k"], lut["n"], lut["group"]
+        runs = []
+        for m, (a, want) in sorted(lut["runs"].items()):
+            nbytes = n * k // 2 + m * k + 4 * m * n + (n // group) * 16
+            rec = {"m": m}
+            for mode in ("tabulate", "decode_dense"):
+                c = np.full(m * n, -7, np.int32)
+                ms = 1e3 * median_time(lambda: oracle.fast_lut4(m, k, n, a, lut["codes"],
+                                                                lut["books"], group, c,
+                                                                threads=threads, mode=mode))
+                ok = bool(np.array_equal(c, want))
+                c1 = np.full(m * n, -7, np.int32)
+                ms1 = 1e3 * median_time(lambda: oracle.fast_lut4(m, k, n, a, lut["codes"],
+                                                                 lut["books"], group, c1,
+                                                                 groups=28, threads=1,
+                                                                 mode=mode), runs=3) * 8
+                rec[mode] = {"ms_per_call": round(ms, 3), "GB_s": round(nbytes / ms / 1e6, 2),
+                             "one_core_ms_extrapolated": round(ms1, 2),
+                             "bytes_equal_gpu": ok}
+            best = min(("tabulate", "decode_dense"), key=lambda md: rec[md]["ms_per_call"])
+            rec["best"] = best
+            runs.append(rec)
+        out["lut"] = {"unit": "GB/s of algorithmic bytes", "cores": threads, "kind": "port",
+                      "runs": runs}
+    trop = CPU_INPUTS.get("trop")
+    if trop:
+        N = trop["N"]
+        c = np.full(N * N * 8, 0xEE, np.uint8)
+        dt = median_time(lambda: oracle.fast_trop_i8(N, N, N, trop["a"], trop["b"], c,
+                                                    threads=threads), runs=3)
+        g, w = c.reshape(-1, 8), trop["c"].reshape(-1, 8)
+        ok = bool(np.array_equal(g[:, :5], w[:, :5]))
+        c1 = np.full(N * N * 8, 0xEE, np.uint8)
+        rows1 = 256
+        dt1 = median_time(lambda: oracle.fast_trop_i8(N, N, N, trop["a"], trop["b"], c1, rows=rows1,
+                                                     threads=1), runs=1)
+        out["trop"] = {"value": round(float(N) ** 3 / dt / 1e12, 4), "unit": "Tterm/s",
+                       "cores": threads, "kind": "port", "ms_per_call": round(dt * 1e3, 1),
+                       "sample": "the whole 4096^3 product", "bytes_equal_gpu": ok,
+                       "one_core": {"value": round(rows1 * float(N) ** 2 / dt1 / 1e12, 4),
+                                    "sample": f"rows 0..{rows1}, B packing included"}}
+    for fl in CPU_INPUTS.get("float", []):
+        N, is64 = fl["N"], fl["is64"]
+        ft = np.float64 if is64 else np.float32
+        a, b = fl["a"], fl["b"]
+        rows = 64
+
+        def slab(r0, r1, c):
+            return oracle.gemm_float(a[r0 * N:r1 * N], (r1 - r0, N), (N, 1), b, (N, N), (N, 1),
+                                     c[r0 * N:r1 * N], (r1 - r0, N), (N, 1))
+
+        c = np.full(rows * N, np.nan, ft)
+        cuts = [rows * t // threads for t in range(threads + 1)]
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(threads) as pool:
+            sts = list(pool.map(lambda t: slab(cuts[t], cuts[t + 1], c), range(threads)))
+        dt = time.perf_counter() - t0
+        ok = all(st == "ok" for st in sts) and bool(np.array_equal(
+            c.view(np.uint64 if is64 else np.uint32), fl["c"].view(np.uint64 if is64 else np.uint32)))
+        rows1 = 8
+        c1 = np.full(rows * N, np.nan, ft)
+        t0 = time.perf_counter()
+        slab(0, rows1, c1)
+        dt1 = time.perf_counter() - t0
+        full_s = dt * N / rows
+        out.setdefault("float", []).append({
+            "format": "f64" if is64 else "f32", "m": N, "n": N, "k": N,
+            "value": round(2.0 * N ** 3 / full_s / 1e9, 3), "unit": "exact GFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"rows 0..{rows} in {dt:.2f} s, extrapolated x{N // rows} "
+                      "(rows are independent)",
+            "full_problem_s_extrapolated": round(full_s, 1),
+            "ns_per_product_per_core": round(dt * threads / (rows * N * N) * 1e9, 2),
+            "bytes_equal_gpu": ok,
+            "one_core": {"value": round(2.0 * rows1 * N * N / dt1 / 1e9, 3),
+                         "sample": f"rows 0..{rows1} in {dt1:.2f} s"}})
+    return out
 
 
 PARTS = ["i8", "config1", "deep", "lut", "prefill", "coded", "collapse", "trop", "float", "int",
@@ -847,6 +998,7 @@ def main():
             parts.discard("int")
         if args.no_cpu_baseline:
             parts.discard("cpu")
+    args.parts = parts
     import torch
     if args.copy_calibration:
         n = 1 << 30
@@ -929,6 +1081,10 @@ def main():
         from oracle import oracle
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline_i8(host, oracle)
+    if "cpu" in parts and CPU_INPUTS:
+        from oracle import oracle
+        log("[bench] cpu baselines, secondary configs")
+        result["cpu_baselines_secondary"] = cpu_baselines_secondary(oracle)
     print(json.dumps(result), flush=True)
 
 

@@ -194,6 +194,11 @@ def fast():
         F.fr_gemm_i8_i32.argtypes = [_i32, _i32, _i32, _i64, _vp, _i64, _vp, _i64, _i64, _vp,
                                      _i64, _i32, _i32, _i32, _i32]
         F.fr_gemm_i8_i32.restype = _i32
+        F.fr_lut4.argtypes = [_i32, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _vp, _i64, _i32,
+                              _i32, _i32]
+        F.fr_lut4.restype = _i32
+        F.fr_trop_i8.argtypes = [_i32, _i32, _i32, _vp, _vp, _vp, _i32, _i32, _i32]
+        F.fr_trop_i8.restype = _i32
         _fast = F
     return _fast
 
@@ -203,6 +208,22 @@ def fast_gemm_i8_i32(m, k, n, alpha, a, lda, b, ldb, beta, c, ldc, row0=0, rows=
     rows = m if rows is None else rows
     return fast().fr_gemm_i8_i32(m, k, n, int(alpha), _ptr(a), lda, _ptr(b), ldb, int(beta),
                                  _ptr(c), ldc, row0, rows, threads, int(force_avx2))
+
+
+def fast_lut4(m, k, n, a, codes, books, group, c, groups=None, threads=1, mode="tabulate"):
+    """The table-lookup product on the CPU baseline: A (m x k i8, row-major),
+    codes (n x k/2 bytes), one 16-entry book per `group` rows of W, C (m x n
+    i32).  `groups` limits the run to the first groups (a bounded sample)."""
+    groups = n // group if groups is None else groups
+    return fast().fr_lut4(m, k, n, _ptr(a), k, _ptr(codes), _ptr(books), group, _ptr(c), n,
+                          groups, threads, {"tabulate": 0, "decode_dense": 1}[mode])
+
+
+def fast_trop_i8(m, k, n, a, b, c, row0=0, rows=None, threads=1):
+    """Max-plus on the CPU baseline: Trop<i8> records in, Trop<i32> out
+    (default MaxPlus), rows [row0, row0 + rows)."""
+    rows = m if rows is None else rows
+    return fast().fr_trop_i8(m, k, n, _ptr(a), _ptr(b), _ptr(c), row0, rows, threads)
 
 
 # ------------------------------------------------------------------- codecs

@@ -35,3 +35,48 @@ def test_fastroute_slab(oracle):
     oracle.fast_gemm_i8_i32(m, k, n, 1, a, k, b, n, 0, slab, n, row0=128, rows=64, threads=2)
     s = slice(128 * n, 192 * n)
     assert np.array_equal(slab[s], full[s]) and not slab[:128 * n].any()
+
+
+@pytest.mark.parametrize("mode", ["tabulate", "decode_dense"])
+@pytest.mark.parametrize("m", [1, 3, 8, 19])
+def test_fastroute_lut4_matches_oracle(oracle, m, mode):
+    k, n, group = 256, 96, 32
+    rng = np.random.default_rng(m)
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    codes = rng.integers(0, 256, n * k // 2).astype(np.uint8)
+    books = rng.integers(-128, 128, (n // group) * 16).astype(np.int8)
+    books[:16] = -128                       # the extreme pair sum, 2 * 128 * 128
+    a[:k] = -128
+    want = np.zeros(m * n, np.int32)
+    assert oracle.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, want, (n, 1)) == "ok"
+    got = np.full(m * n, 7, np.int32)
+    assert oracle.fast_lut4(m, k, n, a, codes, books, group, got, threads=2, mode=mode) == 0
+    assert np.array_equal(got, want)
+    # A bounded sample: the first group only.
+    part = np.full(m * n, 7, np.int32)
+    assert oracle.fast_lut4(m, k, n, a, codes, books, group, part, groups=1, mode=mode) == 0
+    g = part.reshape(m, n)
+    assert np.array_equal(g[:, :group], want.reshape(m, n)[:, :group]) and (g[:, group:] == 7).all()
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 16), (5, 37, 32), (33, 300, 64)])
+def test_fastroute_trop_matches_oracle(oracle, shape):
+    m, k, n = shape
+    rng = np.random.default_rng(k)
+
+    def recs(count):
+        r = np.zeros((count, 2), np.uint8)
+        r[:, 0] = rng.integers(0, 256, count)
+        r[:, 1] = rng.random(count) > 0.3
+        return r.reshape(-1)
+
+    a, b = recs(m * k), recs(k * n)
+    a[0:2] = [0x80, 1]                      # -128, the lane's lowest finite value
+    b.reshape(k, n, 2)[:, 1, 1] = 0         # column 1 is -inf in every row
+    want = np.zeros(m * n * 8, np.uint8)
+    assert oracle.gemm_trop(a, (m, k), (k, 1), b, (k, n), (n, 1), want, (m, n), (n, 1)) == "ok"
+    got = np.full(m * n * 8, 0xEE, np.uint8)
+    assert oracle.fast_trop_i8(m, k, n, a, b, got, threads=3) == 0
+    g, w = got.reshape(-1, 8), want.reshape(-1, 8)
+    assert np.array_equal(g[:, :5], w[:, :5])
+    assert not w[:, 4].all() and w[:, 4].any()
