@@ -83,7 +83,10 @@ def test_alpha_beta(oracle, uor, dev, is64, offer):
     c0 = (rng.standard_normal(m * n) * 2.0 ** rng.integers(-60, 60, m * n)).astype(ft)
     c0[[3, 7, 11, 12, 50]] = [np.inf, -np.inf, np.nan, 0.0, -0.0]
     for alpha, beta in [(1, 1), (3, -1), (0, 2), (-7, 0), (1 << 40, -(1 << 50)), (0, 0),
-                        (-(1 << 63), 1), ((1 << 63) - 1, -(1 << 63))]:
+                        (-(1 << 63), 1), ((1 << 63) - 1, -(1 << 63)),
+                        # beta = 0 with |alpha| at the register window's 32-bit
+                        # limit and just past it (the LDS-register kernel).
+                        ((1 << 32) - 1, 0), (-(1 << 32) + 1, 0), (1 << 32, 0), (70000, 0)]:
         for mode in ("nearest", "toward_zero"):
             check(oracle, uor, dev, a, b, m, k, n, c0=c0, alpha=alpha, beta=beta, mode=mode,
                   offer=offer)

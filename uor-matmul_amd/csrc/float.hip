@@ -878,11 +878,12 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
     double f = 0;
     const uint16_t(*Ml)[CRT_ND16] = crt_Ml16[nmod - 1];
     const uint16_t *inv = crt_inv[nmod - 1];
-    // G planes' bytes at a time, so their loads overlap (all of them where
-    // registers allow).
-#pragma unroll
-    for (int l0 = 0; l0 < CRT_NMAX; l0 += G) {
-        if (l0 < nmod) {
+    // G planes' bytes at a time, so their loads overlap.  The groups stay a
+    // loop: unrolled, the compiler keeps every group's residues and table rows
+    // live at once (over 200 VGPRs).
+#pragma unroll 1
+    for (int l0 = 0; l0 < nmod; l0 += G) {
+        {
             int yb[G];
 #pragma unroll
             for (int u = 0; u < G; ++u)
@@ -904,7 +905,8 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
                     }
                     f += (double)c * crt_invp[l];
 #pragma unroll
-                    for (int d = 0; d < ND; ++d) sl[d] += c * (int32_t)Ml[l][d];
+                    for (int d = 0; d < ND; ++d)  // c < 2^8, Ml < 2^16: a 24-bit multiply
+                        sl[d] += (int32_t)__umul24((uint32_t)c, (uint32_t)Ml[l][d]);
                 }
             }
         }
@@ -1119,6 +1121,215 @@ __device__ inline void crt_general_cell(const FArgs &F, const Reg &R, const Line
     finish_cell<F64>(F, R, neg, flags, i, j, wlo, whi);
 }
 
+// ---------------------------------------------- the register-window finish --
+//
+// The CRT cells the register epilogue does not take, when beta = 0 and
+// |alpha| < 2^32: the diagonals combine by Horner's rule from the top,
+// T := T * 2^w + X_d, in a two's-complement window of NW 32-bit words held in
+// VGPRs (the value is T * 2^E, E = the lines' lo exponents), then alpha and
+// one rounding.  The window holds w * (diagonals - 1) + 16 * ND bits plus 32
+// bits for alpha and two of sign and carry; the plan's w and diagonal count
+// are uniform, so the shifts are the same for every lane.  Cells whose window
+// would not fit, and every cell when beta != 0, take the LDS-register kernel.
+
+constexpr int WIN_MAX_WORDS = 48;
+
+// The window bits a plan needs at ND digits per diagonal.
+__host__ __device__ inline int window_bits(const CrtHdr &hd, int nd) {
+    const int ndiag = hd.sa + hd.sb - 1;
+    return (ndiag > 1 ? hd.w * (ndiag - 1) : 0) + 16 * nd + 34;
+}
+
+__device__ inline int crt_nd_template(int nmod) {
+    const int nd = crt_nd16[nmod];
+    return nd <= 8 ? 8 : nd <= 12 ? 12 : nd <= 16 ? 16 : nd <= 20 ? 20 : CRT_ND16;
+}
+
+__device__ inline bool window_cell(const FArgs &F, const CrtHdr &hd, const LineStat &sa,
+                                   const LineStat &sb) {
+    const uint64_t fa = F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha;
+    return !hd.crt_off && !fast_cell(F, hd, sa, sb) && F.beta == 0 && (fa >> 32) == 0 &&
+           window_bits(hd, crt_nd_template(hd.nmod)) <= 32 * WIN_MAX_WORDS;
+}
+
+// impl_encode_into_float (acc.rs:1734-1868) from a magnitude in NW 32-bit
+// words T[] whose bit 0 has exponent E: encode16's rounding, read from words.
+template <bool F64, int NW>
+__device__ inline uint64_t encode32(const uint32_t (&T)[NW], int E, bool neg, int mode) {
+    using Fm = Fmt<F64>;
+    constexpr int MANT = Fm::MANT, EXPO = Fm::EXPO, P = MANT + 1;
+    constexpr uint64_t EXPMASK = (1ull << EXPO) - 1;
+    int top = -1;
+#pragma unroll
+    for (int t = 0; t < NW; ++t)
+        if (T[t]) top = 32 * t + 31 - __builtin_clz(T[t]);
+    if (top < 0) return 0;  // an exact zero is +0
+    const int exp = E + top;
+    int lsb_exp = exp - (P - 1) < Fm::SUB_LSB ? Fm::SUB_LSB : exp - (P - 1);
+    const int lsb = lsb_exp - E;
+    uint64_t sig;
+    int round_bit = 0, sticky = 0;
+    if (lsb <= 0) {
+        // Every bit lies at or above the output's LSB: the value is below 2^P.
+        sig = ((uint64_t)T[0] | (NW > 1 ? (uint64_t)T[1 < NW ? 1 : 0] << 32 : 0)) << (-lsb);
+    } else {
+        const int q = lsb >> 5, r = lsb & 31;
+        const int rb = lsb - 1, qb = rb >> 5;
+        const uint32_t below = (1u << (rb & 31)) - 1;
+        uint64_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t v = T[t];
+            w0 = t == q ? v : w0;
+            w1 = t == q + 1 ? v : w1;
+            w2 = t == q + 2 ? v : w2;
+            if (t == qb) {
+                round_bit = (int)((v >> (rb & 31)) & 1);
+                if (v & below) sticky = 1;
+            }
+            if (t < qb && v) sticky = 1;
+        }
+        const uint64_t lo = w0 | (w1 << 32);
+        sig = ((lo >> r) | (r ? (w2 << (64 - r)) : 0)) & ((1ull << P) - 1);
+    }
+    const int inc = (mode == UOR_ENCODE_NEAREST) ? (round_bit && (sticky || (sig & 1))) : 0;
+    sig += (uint64_t)inc;
+    if (sig >> P) {
+        sig >>= 1;
+        lsb_exp += 1;
+    }
+    const uint64_t sbit = (uint64_t)(neg ? 1 : 0) << (MANT + EXPO);
+    if (sig == 0) return sbit;
+    if ((sig >> (P - 1)) == 1) {
+        const int biased = lsb_exp + (P - 1) + Fm::BIAS;
+        if (biased >= (int)EXPMASK) {
+            if (mode == UOR_ENCODE_NEAREST) return sbit | (EXPMASK << MANT);
+            return sbit | ((EXPMASK - 1) << MANT) | ((1ull << MANT) - 1);
+        }
+        return sbit | ((uint64_t)biased << MANT) | (sig & ((1ull << MANT) - 1));
+    }
+    return sbit | sig;
+}
+
+// The special values encode_reg gives a cell with non-finite flags.
+template <bool F64>
+__device__ inline uint64_t encode_flags(int flags) {
+    using Fm = Fmt<F64>;
+    if ((flags & FL_NAN) || ((flags & FL_PINF) && (flags & FL_NINF))) return Fm::NAN_BITS;
+    const uint64_t s = (flags & FL_NINF) ? 1 : 0;
+    return (s << (Fm::MANT + Fm::EXPO)) | (((1ull << Fm::EXPO) - 1) << Fm::MANT);
+}
+
+template <bool F64, int ND, int NW>
+__device__ inline void crt_window_cell(const FArgs &F, const LineStat &sa, const LineStat &sb,
+                                       int flags, const CrtHdr &hd, int nm, const uint8_t *y,
+                                       uint64_t y_plane, uint64_t i, uint64_t j) {
+    const int64_t ci = (int64_t)i * F.crs + (int64_t)j * F.ccs;
+    flags = scale_flags(flags, F.alpha);
+    if (flags) {
+        store_bits<F64>(F.c, ci, encode_flags<F64>(flags));
+        return;
+    }
+    uint32_t T[NW];
+#pragma unroll
+    for (int t = 0; t < NW; ++t) T[t] = 0;
+    if (hd.nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY) && F.alpha != 0) {
+        const int ndiag = hd.sa + hd.sb - 1;
+        const int qw = hd.w >> 5, r = hd.w & 31;
+        for (int dg = ndiag - 1; dg >= 0; --dg) {
+            if (dg != ndiag - 1) {
+                // T <<= w: whole words by stages of 4, 2 and 1, then r bits.
+                if (qw & 4) {
+#pragma unroll
+                    for (int t = NW - 1; t >= 0; --t) T[t] = t >= 4 ? T[t - 4] : 0u;
+                }
+                if (qw & 2) {
+#pragma unroll
+                    for (int t = NW - 1; t >= 0; --t) T[t] = t >= 2 ? T[t - 2] : 0u;
+                }
+                if (qw & 1) {
+#pragma unroll
+                    for (int t = NW - 1; t >= 0; --t) T[t] = t >= 1 ? T[t - 1] : 0u;
+                }
+                if (r) {
+#pragma unroll
+                    for (int t = NW - 1; t >= 1; --t)
+                        T[t] = __builtin_amdgcn_alignbit(T[t], T[t - 1], 32 - r);
+                    T[0] <<= r;
+                }
+            }
+            uint32_t D[ND];
+            const bool negx = crt16<ND>(y + (uint64_t)dg * nm * y_plane, y_plane, i * F.n + j,
+                                        hd.nmod, D);
+            // T += (-1)^negx X, two's complement over the whole window.
+            const uint32_t xm = negx ? 0xffffffffu : 0u;
+            uint32_t c = negx ? 1u : 0u;
+#pragma unroll
+            for (int t = 0; t < NW; ++t) {
+                uint32_t x = 0;
+                if (2 * t < ND) x = D[2 * t] | (2 * t + 1 < ND ? D[2 * t + 1] << 16 : 0u);
+                const uint64_t s = (uint64_t)T[t] + (x ^ xm) + c;
+                T[t] = (uint32_t)s;
+                c = (uint32_t)(s >> 32);
+            }
+        }
+    }
+    bool neg = (T[NW - 1] >> 31) != 0;
+    if (neg) {
+        uint32_t c = 1;
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint64_t s = (uint64_t)(~T[t]) + c;
+            T[t] = (uint32_t)s;
+            c = (uint32_t)(s >> 32);
+        }
+    }
+    const uint32_t fa = (uint32_t)(F.alpha < 0 ? (uint64_t)0 - (uint64_t)F.alpha : (uint64_t)F.alpha);
+    if (fa != 1) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint64_t v = (uint64_t)T[t] * fa + c;
+            T[t] = (uint32_t)v;
+            c = (uint32_t)(v >> 32);
+        }
+    }
+    if (F.alpha < 0) neg = !neg;
+    store_bits<F64>(F.c, ci, encode32<F64, NW>(T, sa.lo + sb.lo, neg, F.mode));
+}
+
+template <bool F64, int ND>
+__device__ inline void crt_window_dispatch(const FArgs &F, const LineStat &sa, const LineStat &sb,
+                                           int flags, const CrtHdr &hd, int nm, const uint8_t *y,
+                                           uint64_t y_plane, uint64_t i, uint64_t j) {
+    const int bits = window_bits(hd, ND);
+    if (bits <= 32 * 16) crt_window_cell<F64, ND, 16>(F, sa, sb, flags, hd, nm, y, y_plane, i, j);
+    else if (bits <= 32 * 32) crt_window_cell<F64, ND, 32>(F, sa, sb, flags, hd, nm, y, y_plane, i, j);
+    else crt_window_cell<F64, ND, WIN_MAX_WORDS>(F, sa, sb, flags, hd, nm, y, y_plane, i, j);
+}
+
+template <bool F64, int TM, int TN>
+__global__ void __launch_bounds__(TM * TN) crt_window_kernel(FArgs F, const LineStat *ra,
+                                                             const LineStat *cb, const CrtHdr *h,
+                                                             const uint8_t *y, uint64_t y_plane,
+                                                             int nm, int gn) {
+    const int t = threadIdx.x;
+    const uint64_t i = (uint64_t)(blockIdx.x / gn) * TM + t / TN;
+    const uint64_t j = (uint64_t)(blockIdx.x % gn) * TN + t % TN;
+    if (i >= F.m || j >= F.n) return;
+    const CrtHdr hd = *h;
+    const LineStat sa = ra[i], sb = cb[j];
+    if (!window_cell(F, hd, sa, sb)) return;
+    const int flags = ((sa.flags | sb.flags) & LS_DIRTY) ? flags_cell<F64>(F, i, j) : 0;
+    switch (crt_nd_template(hd.nmod)) {
+    case 8: crt_window_dispatch<F64, 8>(F, sa, sb, flags, hd, nm, y, y_plane, i, j); break;
+    case 12: crt_window_dispatch<F64, 12>(F, sa, sb, flags, hd, nm, y, y_plane, i, j); break;
+    case 16: crt_window_dispatch<F64, 16>(F, sa, sb, flags, hd, nm, y, y_plane, i, j); break;
+    case 20: crt_window_dispatch<F64, 20>(F, sa, sb, flags, hd, nm, y, y_plane, i, j); break;
+    default: crt_window_dispatch<F64, CRT_ND16>(F, sa, sb, flags, hd, nm, y, y_plane, i, j); break;
+    }
+}
+
 template <bool F64, int TM, int TN>
 __global__ void __launch_bounds__(TM * TN) crt_fast_kernel(FArgs F, const LineStat *ra,
                                                            const LineStat *cb, const CrtHdr *h,
@@ -1152,7 +1363,7 @@ __global__ void __launch_bounds__(TM * TN) crt_general_kernel(FArgs F, const Lin
     if (i >= F.m || j >= F.n) return;
     const CrtHdr hd = *h;
     const LineStat sa = ra[i], sb = cb[j];
-    if (fast_cell(F, hd, sa, sb)) return;
+    if (fast_cell(F, hd, sa, sb) || window_cell(F, hd, sa, sb)) return;
     const Reg R{regs + t, NT};
     if (hd.crt_off) {
         for (int q = 0; q < S; ++q) R[q] = 0;
@@ -1272,6 +1483,12 @@ static hipError_t launch_crt(const FArgs &F, char *scratch, const CrtLayout &L, 
         const uint64_t gm = (m + TM - 1) / TM, gn = (n + TN - 1) / TN;
         hipLaunchKernelGGL((crt_fast_kernel<F64, TM, TN>), dim3((unsigned)(gm * gn)), dim3(TM * TN), 0, s, F,
                            ra, cb, h, y, L.y_plane, (int)gn);
+    }
+    {
+        constexpr int TM = 4, TN = 64;
+        const uint64_t gm = (m + TM - 1) / TM, gn = (n + TN - 1) / TN;
+        hipLaunchKernelGGL((crt_window_kernel<F64, TM, TN>), dim3((unsigned)(gm * gn)), dim3(TM * TN), 0, s,
+                           F, ra, cb, h, y, L.y_plane, nm, (int)gn);
     }
     {
         constexpr int TM = F64 ? 1 : 4, TN = 64;
@@ -1746,7 +1963,7 @@ extern "C" int uor_gfx950_gemm_float(int is_f64, const uor_view *a, const uor_vi
             route->tile_m = route->tile_n = 256;
             route->tile_k = DL_BK;
             route->split_k = 1;
-            route->launches = 8;
+            route->launches = 9;
             route->moduli = nm;  // planes offered; the device uses the fewest that suffice
             route->scratch_used = L.total;
         }
