@@ -499,31 +499,41 @@ __device__ inline int bitlen64(uint64_t v) { return 64 - __builtin_clzll(v); }
 // the threads along one line; LPB = 64 (s_line == 1) puts a wave across 64
 // neighbouring lines, one 64-element row segment per load; LPB = 16 is for
 // the other strides.
-template <bool F64, int LPB>
-__global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64_t s_line,
-                                                         int64_t s_elem, uint64_t lines,
-                                                         uint64_t len, LineStat *out) {
-    constexpr int TPL = 256 / LPB;  // threads per line
-    __shared__ int s_lo[256], s_hi[256], s_fl[256];
-    __shared__ double s_sum[256];
+template <bool F64, int LPB, int NT = 256>
+__global__ void __launch_bounds__(NT) line_stats_kernel(const char *base, int64_t s_line,
+                                                        int64_t s_elem, uint64_t lines,
+                                                        uint64_t len, LineStat *out) {
+    constexpr int TPL = NT / LPB;  // threads per line
+    constexpr int U = 4;           // loads in flight per thread
+    __shared__ int s_lo[NT], s_hi[NT], s_fl[NT];
+    __shared__ double s_sum[NT];
     const int t = threadIdx.x;
     const int tl = t % LPB, te = t / LPB;
     const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
     const bool live = line < lines;
     int lo = 1 << 30, hi = -(1 << 30), fl = 0;
     if (live) {
-        for (uint64_t e = te; e < len; e += TPL) {
-            const Dec d = decode<F64>(load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
-            if (d.cls != CLS_FINITE) {
-                fl |= LS_DIRTY;
-                continue;
+        for (uint64_t e0 = te; e0 < len; e0 += (uint64_t)TPL * U) {
+            uint64_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint64_t e = e0 + (uint64_t)u * TPL;
+                v[u] = e < len ? load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem) : 0;
             }
-            if (!d.mant) continue;
-            uint64_t m;
-            int x;
-            trim(d, &m, &x);
-            lo = min(lo, x);
-            hi = max(hi, x + bitlen64(m));
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const Dec d = decode<F64>(v[u]);
+                if (d.cls != CLS_FINITE) {
+                    fl |= LS_DIRTY;
+                    continue;
+                }
+                if (!d.mant) continue;
+                uint64_t m;
+                int x;
+                trim(d, &m, &x);
+                lo = min(lo, x);
+                hi = max(hi, x + bitlen64(m));
+            }
         }
     }
     s_lo[t] = lo;
@@ -545,13 +555,22 @@ __global__ void __launch_bounds__(256) line_stats_kernel(const char *base, int64
     // Pass 2: sum of |aligned integers| scaled by 2^-(top), each term <= 1.
     double sum = 0;
     if (live && hi > lo) {
-        for (uint64_t e = te; e < len; e += TPL) {
-            const Dec d = decode<F64>(load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
-            if (d.cls != CLS_FINITE || !d.mant) continue;
-            uint64_t m;
-            int x;
-            trim(d, &m, &x);
-            sum += ldexp((double)m, x - hi);
+        for (uint64_t e0 = te; e0 < len; e0 += (uint64_t)TPL * U) {
+            uint64_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint64_t e = e0 + (uint64_t)u * TPL;
+                v[u] = e < len ? load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem) : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const Dec d = decode<F64>(v[u]);
+                if (d.cls != CLS_FINITE || !d.mant) continue;
+                uint64_t m;
+                int x;
+                trim(d, &m, &x);
+                sum += ldexp((double)m, x - hi);
+            }
         }
     }
     __syncthreads();
@@ -661,11 +680,18 @@ __global__ void __launch_bounds__(256) crt_plan_kernel(const LineStat *ra, uint6
     *h = r;
 }
 
-// Balanced int8 residue of +-m * 2^s modulo crt_mod[l] (s < 256).  For
-// m < 2^45 the product m * (2^s mod p) < 2^53 is exact in a double and one
-// reduction suffices (the quotient's rounding error is below one); a wider m
-// (f64 significands) is first reduced alone.  An f32 significand (< 2^24)
-// keeps the product below 2^32.
+// x mod p for x < 2^25 and p < 2^8: the single-precision quotient of such an
+// x is off by at most one, which one correction each way absorbs.
+__device__ inline uint32_t mod_small(uint32_t x, int p, float ip) {
+    int r = (int)x - (int)((float)x * ip) * p;
+    if (r < 0) r += p;
+    if (r >= p) r -= p;
+    return (uint32_t)r;
+}
+
+// Balanced int8 residue of +-m * 2^s modulo crt_mod[l] (s < 256).  An f32
+// significand (< 2^24) keeps m * (2^s mod p) below 2^32, reduced through a
+// double; an f64 one is reduced in 24-bit limbs with mod_small.
 template <bool F64>
 __device__ inline int residue(uint64_t m, int s, bool neg, int l, const uint8_t *pow2) {
     const int p = crt_mod[l];
@@ -680,20 +706,14 @@ __device__ inline int residue(uint64_t m, int s, bool neg, int l, const uint8_t 
         if (r < 0) r += p;
         if (r >= p) r -= p;
     } else {
-        const double ip = crt_invp[l];
-        if (m >> 45) {
-            const double q0 = floor((double)m * ip);
-            int64_t r0 = (int64_t)m - (int64_t)q0 * p;
-            if (r0 < 0) r0 += p;
-            if (r0 >= p) r0 -= p;
-            m = (uint64_t)r0;
-        }
-        const int64_t x = (int64_t)(m * (uint64_t)w);
-        const double q = floor((double)x * ip);
-        int64_t rr = x - (int64_t)q * p;
-        if (rr < 0) rr += p;
-        if (rr >= p) rr -= p;
-        r = (int)rr;
+        // m < 2^53 in three 24-bit limbs: m mod p = (m0 + (m1 mod p) 2^24 +
+        // m2 2^48) mod p, every step a reduction of a value below 2^25.
+        const float ip = crt_invpf[l];
+        const uint32_t m0 = (uint32_t)m & 0xffffffu, m1 = (uint32_t)(m >> 24) & 0xffffffu,
+                       m2 = (uint32_t)(m >> 48);
+        const uint32_t t = m0 + mod_small(m1, p, ip) * pow2[l * 256 + 24] +
+                           m2 * pow2[l * 256 + 48];
+        r = (int)mod_small(mod_small(t, p, ip) * w, p, ip);
     }
     int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
     if (neg) b = -b;
@@ -878,36 +898,41 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
     double f = 0;
     const uint16_t(*Ml)[CRT_ND16] = crt_Ml16[nmod - 1];
     const uint16_t *inv = crt_inv[nmod - 1];
-    // G planes' bytes at a time, so their loads overlap.  The groups stay a
-    // loop: unrolled, the compiler keeps every group's residues and table rows
-    // live at once (over 200 VGPRs).
+    // G planes' bytes at a time, the next group's loads issued before this
+    // group's arithmetic (clamped to the last plane, so every load is in
+    // bounds and none is conditional).  The groups stay a loop: unrolled, the
+    // compiler keeps every group's residues and table rows live at once (over
+    // 200 VGPRs).
+    const uint8_t *yc = y + cell;
+    int nxt[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) nxt[u] = yc[(uint64_t)min(u, nmod - 1) * y_plane];
 #pragma unroll 1
     for (int l0 = 0; l0 < nmod; l0 += G) {
-        {
-            int yb[G];
+        int yb[G];
 #pragma unroll
-            for (int u = 0; u < G; ++u)
-                yb[u] = (l0 + u < CRT_NMAX && l0 + u < nmod) ? (int)y[(uint64_t)(l0 + u) * y_plane + cell] : 0;
+        for (int u = 0; u < G; ++u) yb[u] = nxt[u];
 #pragma unroll
-            for (int u = 0; u < G; ++u) {
-                const int l = l0 + u;
-                if (l < CRT_NMAX && l < nmod) {
-                    const int p = crt_mod[l];
-                    const int prod = yb[u] * (int)inv[l];  // < 2^16
-                    int c;
-                    if (l == 0) {
-                        c = prod & 255;
-                    } else {
-                        const int q = (int)((float)prod * crt_invpf[l]);
-                        c = prod - q * p;
-                        if (c < 0) c += p;
-                        if (c >= p) c -= p;
-                    }
-                    f += (double)c * crt_invp[l];
+        for (int u = 0; u < G; ++u) nxt[u] = yc[(uint64_t)min(l0 + G + u, nmod - 1) * y_plane];
 #pragma unroll
-                    for (int d = 0; d < ND; ++d)  // c < 2^8, Ml < 2^16: a 24-bit multiply
-                        sl[d] += (int32_t)__umul24((uint32_t)c, (uint32_t)Ml[l][d]);
+        for (int u = 0; u < G; ++u) {
+            const int l = l0 + u;
+            if (l < CRT_NMAX && l < nmod) {
+                const int p = crt_mod[l];
+                const int prod = yb[u] * (int)inv[l];  // < 2^16
+                int c;
+                if (l == 0) {
+                    c = prod & 255;
+                } else {
+                    const int q = (int)((float)prod * crt_invpf[l]);
+                    c = prod - q * p;
+                    if (c < 0) c += p;
+                    if (c >= p) c -= p;
                 }
+                f += (double)c * crt_invp[l];
+#pragma unroll
+                for (int d = 0; d < ND; ++d)  // c < 2^8, Ml < 2^16: a 24-bit multiply
+                    sl[d] += (int32_t)__umul24((uint32_t)c, (uint32_t)Ml[l][d]);
             }
         }
     }
@@ -1059,7 +1084,7 @@ __device__ inline void crt_fast_cell(const FArgs &F, const LineStat &sa, const L
     uint32_t D[ND + 1];
     bool neg = false;
     if (nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY)) {
-        neg = crt16<ND + 1, CRT_NMAX>(y, y_plane, i * F.n + j, nmod, D);
+        neg = crt16<ND + 1, 16>(y, y_plane, i * F.n + j, nmod, D);
     } else {
 #pragma unroll
         for (int dd = 0; dd <= ND; ++dd) D[dd] = 0;
@@ -1420,16 +1445,19 @@ static int crt_slice_cap(bool f64, uint64_t k) {
     return s;
 }
 
-// Line statistics with the lanes along a line when it is contiguous, else
-// 16 lines by 16 lanes.  (64 lines by 4 lanes, one 64-element row segment
-// per load, ran 5x slower at 4096 lines of 4096: 64 workgroups whose lanes
-// each wait on 1024 loads in turn.)
+// Line statistics with the lanes along a line when it is contiguous; a wave
+// across 64 neighbouring lines, 16 waves on the line's elements, when
+// neighbouring lines are neighbouring elements (B's columns); else 16 lines
+// by 16 lanes.
 template <bool F64>
 static void launch_line_stats(const char *base, int64_t s_line, int64_t s_elem, uint64_t lines,
                               uint64_t len, LineStat *out, hipStream_t s) {
     if (s_elem == 1)
         hipLaunchKernelGGL((line_stats_kernel<F64, 1>), dim3((unsigned)lines), dim3(256), 0, s, base, s_line,
                            s_elem, lines, len, out);
+    else if (s_line == 1)  // neighbouring lines are neighbouring elements: a wave across 64 lines
+        hipLaunchKernelGGL((line_stats_kernel<F64, 64, 1024>), dim3((unsigned)((lines + 63) / 64)), dim3(1024), 0, s,
+                           base, s_line, s_elem, lines, len, out);
     else
         hipLaunchKernelGGL((line_stats_kernel<F64, 16>), dim3((unsigned)((lines + 15) / 16)), dim3(256), 0, s,
                            base, s_line, s_elem, lines, len, out);
