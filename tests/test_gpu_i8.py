@@ -344,12 +344,14 @@ def test_fused_tile_epilogues(uor, dev, case):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096 + 36, 4096 + 48, 64), (4096, 4096 + 16, 192),
-                                   (4300, 4112, 320), (4096, 4096, 896), (4352, 4096, 8192 + 64)])
+                                   (4300, 4112, 320), (4096, 4096, 896), (4352, 4096, 8192 + 64),
+                                   (4096 + 36, 4096 + 48, 128), (4096, 4096 + 16, 256),
+                                   (4300, 4112, 384), (4352, 4096, 8192 + 128)])
 def test_tile256_ragged_edges_and_depths(uor, dev, m, n, k):
     """The 256x256 direct-to-LDS tile at ragged m and n (partial edge tiles,
     rows and columns past the edge computed and discarded) and depths of 1, 3,
-    5, 14 and 129 steps of 64 (each remainder of the four-stage loop), with
-    alpha = 3, beta = -1.  Expected values from an exact float64 product
+    5, 14 and 129 steps of 64 and of 2, 4, 6 and 130 (each remainder of the
+    four-stage loop, odd and even), with alpha = 3, beta = -1.  Expected values from an exact float64 product
     (|sum| <= k * 2^14 < 2^53)."""
     lda, ldb, ldc = k + 16, n + 16, n + 8
     rng = np.random.default_rng(m * 7 + n * 3 + k)
@@ -365,6 +367,38 @@ def test_tile256_ragged_edges_and_depths(uor, dev, m, n, k):
     C0 = c0.reshape(m, ldc).astype(np.int64)
     want = 3 * S - C0[:, :n]
     got = c.cpu().numpy().reshape(m, ldc)
+    assert np.array_equal(got[:, :n].astype(np.int64), want)
+    assert np.array_equal(got[:, n:], c0.reshape(m, ldc)[:, n:])
+
+
+@pytest.mark.parametrize("m,n,k", [(2048 + 40, 1024 + 48, 64), (2048, 2048 + 8, 192),
+                                   (1024 + 3, 4096, 320), (2048, 2048, 4096 + 64)])
+@pytest.mark.parametrize("out", ["i32", "i8"])
+def test_tile256_column_major_b(uor, dev, m, n, k, out):
+    """The 256x256 tile with B k-contiguous (column-major, ldb = k + 16): its
+    stage half in A's layout.  Ragged m and n, depths of 1, 3, 5 and 65 steps,
+    alpha = 3, beta = -1, against an exact float64 product; the i8 output
+    saturates."""
+    lda, ldb, ldc = k + 16, k + 16, n + 8
+    rng = np.random.default_rng(m * 5 + n * 3 + k)
+    a = torch.from_numpy(rng.integers(-128, 128, m * lda).astype(np.int8)).to(dev)
+    bt = torch.from_numpy(rng.integers(-128, 128, n * ldb).astype(np.int8)).to(dev)
+    dt, tdt = (np.int32, torch.int32) if out == "i32" else (np.int8, torch.int8)
+    c0 = rng.integers(-(1 << 20), 1 << 20, m * ldc).astype(np.int32) if out == "i32" else \
+        rng.integers(-128, 128, m * ldc).astype(np.int8)
+    c = torch.from_numpy(c0.copy()).to(dev)
+    st, route = uor.gemm_i8(a, (m, k), (lda, 1), bt, (k, n), (1, ldb), c, (m, n), (ldc, 1), out=out,
+                            alpha=3, beta=-1, encode="saturating")
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == 256, route
+    assert route["operand_modes"] >> 4 & 1, route  # the direct-to-LDS pipeline
+    S = (a.view(m, lda)[:, :k].double() @ bt.view(n, ldb)[:, :k].double().t()).cpu().numpy()
+    C0 = c0.reshape(m, ldc).astype(np.int64)
+    want = 3 * S.astype(np.int64) - C0[:, :n]
+    lo, hi = (-(1 << 31), (1 << 31) - 1) if out == "i32" else (-128, 127)
+    want = np.clip(want, lo, hi)
+    got = c.cpu().numpy().reshape(m, ldc)
+    assert got.dtype == dt
     assert np.array_equal(got[:, :n].astype(np.int64), want)
     assert np.array_equal(got[:, n:], c0.reshape(m, ldc)[:, n:])
 

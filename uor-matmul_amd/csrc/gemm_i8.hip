@@ -27,8 +27,6 @@
 
 #include <mutex>
 
-#include <type_traits>
-
 #include "mfma_dl.hpp"
 
 namespace uor {
@@ -702,8 +700,10 @@ __device__ inline void buf_store(__amdgpu_buffer_rsrc_t r, int vo, int so, int64
     }
 }
 
+// (Always inlined: a call would pass the uniform strides in VGPRs, which the
+// "s" constraint below cannot take.)
 template <int OB, bool RD>
-__device__ inline void s4_epilogue_full(const OutArgs &out, const v16i (&acc)[4][4], char *corner, int vo,
+__device__ __attribute__((always_inline)) inline void s4_epilogue_full(const OutArgs &out, const v16i (&acc)[4][4], char *corner, int vo,
                                         int srs, int scs) {
     typedef typename std::conditional<OB == 8, int64_t, int32_t>::type P;
     constexpr int NB = OB == 8 ? 1 : 2;  // prior batches in flight
@@ -748,7 +748,7 @@ __device__ inline void s4_epilogue_full(const OutArgs &out, const v16i (&acc)[4]
 }
 
 template <int OB>
-__device__ inline void s4_epilogue_fast(const OutArgs &out, const v16i (&acc)[4][4], uint64_t rw, uint64_t cw,
+__device__ __attribute__((always_inline)) inline void s4_epilogue_fast(const OutArgs &out, const v16i (&acc)[4][4], uint64_t rw, uint64_t cw,
                                         uint64_t M, uint64_t N) {
     const int lane = threadIdx.x & 63, half = lane >> 5, l32 = lane & 31;
     const bool inside = rw + 128 <= M && cw + 128 <= N;
@@ -774,7 +774,8 @@ __device__ inline void s4_epilogue_fast(const OutArgs &out, const v16i (&acc)[4]
             }
 }
 
-template <bool FAST, int OB>
+// BT: B k-contiguous (column-major), staged in A's layout.
+template <bool FAST, int OB, bool BT = false>
 __global__ void __launch_bounds__(256, 1)
 gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
     using L = S4::L;
@@ -793,10 +794,10 @@ gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
 
     S4Lane ln;
     S4Scalars sc;
-    s4_setup_lane(B, lds, ln, sc);
+    s4_setup_lane<BT>(B, lds, ln, sc);
     int tm, tn;
     tile_coords(tile, gm, gn, &tm, &tn);
-    s4_setup_tile(A, B, (uint64_t)tm * 256, (uint64_t)tn * 256, 0, ln, sc);
+    s4_setup_tile<BT>(A, B, (uint64_t)tm * 256, (uint64_t)tn * 256, 0, ln, sc);
     s4_prologue(ln, sc, nk);
     for (;;) {
         v16i acc[4][4];
@@ -804,7 +805,7 @@ gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
-        s4_loop(ln, sc, nk, acc);
+        s4_loop<BT>(ln, sc, nk, acc);
         stage_barrier();  // every wave's stage reads retired: the slots are free
         const uint64_t rw = (uint64_t)tm * 256 + wm * 128, cw = (uint64_t)tn * 256 + wn * 128;
         const int next = tile + (int)gridDim.x;
@@ -812,7 +813,7 @@ gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
         if (next < ntiles) tile_coords(next, gm, gn, &nm, &nn);
         if constexpr (DIRECT) {
             if (next < ntiles) {
-                s4_setup_tile(A, B, (uint64_t)nm * 256, (uint64_t)nn * 256, 0, ln, sc);
+                s4_setup_tile<BT>(A, B, (uint64_t)nm * 256, (uint64_t)nn * 256, 0, ln, sc);
                 s4_prologue(ln, sc, nk);
             }
             s4_epilogue_fast<OB>(out, acc, rw, cw, A.mn, B.mn);
@@ -835,7 +836,7 @@ gemm_i8_s4_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, int gm, int gn) {
             }
             __syncthreads();
             if (next < ntiles) {
-                s4_setup_tile(A, B, (uint64_t)nm * 256, (uint64_t)nn * 256, 0, ln, sc);
+                s4_setup_tile<BT>(A, B, (uint64_t)nm * 256, (uint64_t)nn * 256, 0, ln, sc);
                 s4_prologue(ln, sc, nk);
             }
         }
@@ -1038,14 +1039,14 @@ static int device_cus() {
     return cus;
 }
 
-template <bool FAST>
+template <bool FAST, bool BT = false>
 static hipError_t launch_s4(const Opnd &A, const Opnd &B, const OutArgs &out, uint64_t K, hipStream_t s) {
-    auto kern = gemm_i8_s4_kernel<FAST, 4>;
+    auto kern = gemm_i8_s4_kernel<FAST, 4, BT>;
     switch (out.ob) {
-    case 1: kern = gemm_i8_s4_kernel<FAST, 1>; break;
-    case 2: kern = gemm_i8_s4_kernel<FAST, 2>; break;
-    case 8: kern = gemm_i8_s4_kernel<FAST, 8>; break;
-    case 16: kern = gemm_i8_s4_kernel<false, 16>; break;
+    case 1: kern = gemm_i8_s4_kernel<FAST, 1, BT>; break;
+    case 2: kern = gemm_i8_s4_kernel<FAST, 2, BT>; break;
+    case 8: kern = gemm_i8_s4_kernel<FAST, 8, BT>; break;
+    case 16: kern = gemm_i8_s4_kernel<false, 16, BT>; break;
     default: break;
     }
     const int gm = (int)((A.mn + 255) / 256), gn = (int)((B.mn + 255) / 256);
@@ -1062,6 +1063,15 @@ static bool s4_ok(const Opnd &A, const Opnd &B) {
     if (A.s_mn <= 0 || B.s_k <= 0) return false;
     const unsigned __int128 a_span = (unsigned __int128)A.mn * (uint64_t)A.s_mn + 64;
     const unsigned __int128 b_span = (unsigned __int128)64 * (uint64_t)B.s_k + B.mn + 16;
+    return a_span < ((unsigned __int128)1 << 32) && b_span < ((unsigned __int128)1 << 32);
+}
+
+// The same for a k-contiguous B (column-major, the BT loop): every column of
+// B within 4 GiB of its base.
+static bool s4t_ok(const Opnd &A, const Opnd &B, uint64_t K) {
+    if (A.s_mn <= 0 || B.s_mn <= 0 || B.s_k != 1 || K % DL_BK != 0) return false;
+    const unsigned __int128 a_span = (unsigned __int128)A.mn * (uint64_t)A.s_mn + 64;
+    const unsigned __int128 b_span = (unsigned __int128)B.mn * (uint64_t)B.s_mn + 64;
     return a_span < ((unsigned __int128)1 << 32) && b_span < ((unsigned __int128)1 << 32);
 }
 
@@ -1270,7 +1280,11 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
     // against 0.032 ms).
     const bool use256 = t256 >= 256 || (N >= 128 && t256 >= 32 && (M >= 128 || (M >= 16 && K >= 4096)));
     int bm;
-    if (use256 && dl_ok(pair, K, N)) {
+    if (use256 && pair == 1 && dl_variant() == DL_S4 && s4t_ok(A, B, K)) {
+        bm = 256;
+        UOR_HIP((launch_s4<FAST, true>(A, B, out, K, s)));
+        if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline
+    } else if (use256 && dl_ok(pair, K, N)) {
         bm = 256;
         const int v = dl_variant();
         if (v == DL_S4 && s4_ok(A, B)) {

@@ -401,6 +401,7 @@ struct S4Lane {
     uint32_t voa[4], vob[4];  // global offsets of this lane's A / B chunks (per tile)
     uint32_t ra[2];           // LDS byte address of A fragment 0, k-halves 0 / 1 (stage 0)
     uint32_t rb[4];           // LDS byte address of B fragment j, k-half 0 (stage 0)
+    uint32_t rbt[2];          // BT: LDS byte address of B fragment 0, k-halves 0 / 1
 };
 
 // Scalar state: operand bases at the next stage to load and the LDS targets.
@@ -411,7 +412,12 @@ struct S4Scalars {
     uint32_t mla, mlb; // LDS byte address of this wave's first A / B chunk in stage 0
 };
 
+// BT: B arrives k-contiguous (column-major, B.s_k == 1): its stage half takes
+// A's layout (row = output column, 64 k-bytes) and its fragments are plain
+// 16-byte reads like A's, 8 reads per k-half instead of 12.
+
 // The tile-independent part: fragment read addresses and LDS targets.
+template <bool BT = false>
 __device__ inline void s4_setup_lane(const Opnd &B, const char *lds, S4Lane &ln, S4Scalars &sc) {
     using L = S4::L;
     const int lane = threadIdx.x & 63;
@@ -420,8 +426,10 @@ __device__ inline void s4_setup_lane(const Opnd &B, const char *lds, S4Lane &ln,
     const int half = lane >> 5, l32 = lane & 31, grp = lane >> 4, t16 = lane & 15;
     const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char *)lds;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
         ln.ra[ks] = base + L::a_off(wm * 128 + l32, 2 * ks + half);
+        ln.rbt[ks] = base + L::B_OFF + L::a_off(wn * 128 + l32, 2 * ks + half);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int nb = wn * 128 + 32 * j + 16 * (grp & 1) + 8 * (t16 & 1);
@@ -434,6 +442,7 @@ __device__ inline void s4_setup_lane(const Opnd &B, const char *lds, S4Lane &ln,
 }
 
 // The per-tile part: this lane's chunk offsets and the bases at k = kbeg.
+template <bool BT = false>
 __device__ inline void s4_setup_tile(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t kbeg,
                                      S4Lane &ln, S4Scalars &sc) {
     using L = S4::L;
@@ -448,12 +457,19 @@ __device__ inline void s4_setup_tile(const Opnd &A, const Opnd &B, uint64_t m0, 
         uint64_t gr = m0 + row;
         if (gr >= A.mn) gr = A.mn - 1;  // rows past m are computed and discarded
         ln.voa[i] = (uint32_t)(gr * (uint64_t)A.s_mn + 16 * c);
-        // B chunk: slot = k*16 + physical chunk.
-        const int k = slot >> 4, px = slot & 15;
-        const int x = px ^ L::b_swz(k);
-        uint64_t gn = n0 + 16 * x;
-        if (gn >= B.mn) gn = 0;  // columns past n are computed and discarded
-        ln.vob[i] = (uint32_t)((uint64_t)k * (uint64_t)B.s_k + gn);
+        if constexpr (BT) {
+            // B chunk, A's layout: slot = output column*4 + physical chunk.
+            uint64_t gc = n0 + row;
+            if (gc >= B.mn) gc = B.mn - 1;  // columns past n are computed and discarded
+            ln.vob[i] = (uint32_t)(gc * (uint64_t)B.s_mn + 16 * c);
+        } else {
+            // B chunk: slot = k*16 + physical chunk.
+            const int k = slot >> 4, px = slot & 15;
+            const int x = px ^ L::b_swz(k);
+            uint64_t gn = n0 + 16 * x;
+            if (gn >= B.mn) gn = 0;  // columns past n are computed and discarded
+            ln.vob[i] = (uint32_t)((uint64_t)k * (uint64_t)B.s_k + gn);
+        }
     }
     sc.a = A.base + kbeg;
     sc.b = B.base + (int64_t)kbeg * B.s_k;
@@ -479,11 +495,17 @@ __device__ inline void s4_load(const S4Lane &ln, const S4Scalars &sc, int q) {
 }
 
 // Fragment read number q (0..11) of k-half KS from slot SLOT, in the order
-// A0, B0 lo, B0 hi, A1, B1 lo, B1 hi, ...
-template <int SLOT, int KS>
+// A0, B0 lo, B0 hi, A1, B1 lo, B1 hi, ...; with BT, q in 0..7: A0, B0, A1, ...
+template <int SLOT, int KS, bool BT = false>
 __device__ inline void s4_read(const S4Lane &ln, int q, v4i (&fa)[4], v4i (&fb)[4]) {
     using L = S4::L;
     typedef __attribute__((address_space(3))) const v4i lds_v4i_c;
+    if constexpr (BT) {
+        const int f = q >> 1;
+        if ((q & 1) == 0) fa[f] = *(lds_v4i_c *)(uintptr_t)(ln.ra[KS] + SLOT * L::A_BYTES + f * 32 * 64);
+        else fb[f] = *(lds_v4i_c *)(uintptr_t)(ln.rbt[KS] + SLOT * L::B_BYTES + f * 32 * 64);
+        return;
+    }
     const int f = q / 3, part = q % 3;
     if (part == 0) {
         fa[f] = *(lds_v4i_c *)(uintptr_t)(ln.ra[KS] + SLOT * L::A_BYTES + f * 32 * 64);
@@ -513,17 +535,18 @@ __device__ constexpr int s4_qj(int q) {
 // the same shape: past the last stage the loads repeat the last stage's k
 // (their slot is never read again) and the last step's f0 reads are
 // discarded, so the vmcnt and lgkmcnt accounting is the same in every step.
-template <int CUR>
+template <int CUR, bool BT = false>
 __device__ inline void s4_step(const S4Lane &ln, S4Scalars &sc, bool advance, v4i (&fa0)[4], v4i (&fb0)[4],
                                v4i (&fa1)[4], v4i (&fb1)[4], v16i (&acc)[4][4]) {
     constexpr int NXT = (CUR + 1) & 3, FREE = (CUR + 3) & 3;
+    constexpr int NR = BT ? 8 : 12;  // fragment reads per k-half
     // P1
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
         acc[s4_qi(q)][s4_qj(q)] =
             __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[s4_qi(q)], fb0[s4_qj(q)], acc[s4_qi(q)][s4_qj(q)], 0, 0, 0);
-        if (q < 12) s4_read<CUR, 1>(ln, q, fa1, fb1);
-        else s4_load<FREE>(ln, sc, q - 12);
+        if (q < NR) s4_read<CUR, 1, BT>(ln, q, fa1, fb1);
+        else if (q >= 12) s4_load<FREE>(ln, sc, q - 12);
         S4_FENCE();
     }
     // P2: stage t+1 landed (allowed in flight: stage t+2's eight loads and
@@ -538,8 +561,8 @@ __device__ inline void s4_step(const S4Lane &ln, S4Scalars &sc, bool advance, v4
     for (int q = 0; q < 16; ++q) {
         acc[s4_qi(q)][s4_qj(q)] =
             __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[s4_qi(q)], fb1[s4_qj(q)], acc[s4_qi(q)][s4_qj(q)], 0, 0, 0);
-        if (q < 12) s4_read<NXT, 0>(ln, q, fa0, fb0);
-        else s4_load<FREE>(ln, sc, q - 8);
+        if (q < NR) s4_read<NXT, 0, BT>(ln, q, fa0, fb0);
+        else if (q >= 12) s4_load<FREE>(ln, sc, q - 8);
         S4_FENCE();
     }
     if (advance) {
@@ -567,25 +590,26 @@ __device__ inline void s4_prologue(const S4Lane &ln, S4Scalars &sc, int nk) {
 // must the prologue's stage 0 by the wait below).  Adds into acc, this
 // wave's 128x128 block.  Ends with every load landed and every LDS read of
 // this wave retired, but without a barrier.
+template <bool BT = false>
 __device__ inline void s4_loop(const S4Lane &ln, S4Scalars &sc, int nk, v16i (&acc)[4][4]) {
     v4i fa0[4], fb0[4], fa1[4], fb1[4];
     wait_vm<2 * S4::LOADS>();
     stage_barrier();
     S4_FENCE();
 #pragma unroll
-    for (int q = 0; q < 12; ++q) s4_read<0, 0>(ln, q, fa0, fb0);
+    for (int q = 0; q < (BT ? 8 : 12); ++q) s4_read<0, 0, BT>(ln, q, fa0, fb0);
     S4_FENCE();
     // Step t issues stage t+3 and advances the bases while stage t+4 exists.
     int t = 0;
     for (; t + 4 <= nk; t += 4) {
-        s4_step<0>(ln, sc, t + 4 < nk, fa0, fb0, fa1, fb1, acc);
-        s4_step<1>(ln, sc, t + 5 < nk, fa0, fb0, fa1, fb1, acc);
-        s4_step<2>(ln, sc, t + 6 < nk, fa0, fb0, fa1, fb1, acc);
-        s4_step<3>(ln, sc, t + 7 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<0, BT>(ln, sc, t + 4 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<1, BT>(ln, sc, t + 5 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<2, BT>(ln, sc, t + 6 < nk, fa0, fb0, fa1, fb1, acc);
+        s4_step<3, BT>(ln, sc, t + 7 < nk, fa0, fb0, fa1, fb1, acc);
     }
-    if (t < nk) s4_step<0>(ln, sc, t + 4 < nk, fa0, fb0, fa1, fb1, acc);
-    if (t + 1 < nk) s4_step<1>(ln, sc, t + 5 < nk, fa0, fb0, fa1, fb1, acc);
-    if (t + 2 < nk) s4_step<2>(ln, sc, t + 6 < nk, fa0, fb0, fa1, fb1, acc);
+    if (t < nk) s4_step<0, BT>(ln, sc, t + 4 < nk, fa0, fb0, fa1, fb1, acc);
+    if (t + 1 < nk) s4_step<1, BT>(ln, sc, t + 5 < nk, fa0, fb0, fa1, fb1, acc);
+    if (t + 2 < nk) s4_step<2, BT>(ln, sc, t + 6 < nk, fa0, fb0, fa1, fb1, acc);
     wait_vm<0>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the discarded f0 reads
 }
