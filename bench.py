@@ -189,6 +189,8 @@ def bench_deep(args, torch, uor):
     b = torch.full((k * n,), -128, dtype=torch.int8, device=dev)
     c = torch.zeros(m * n, dtype=torch.int64, device=dev)
     sc = torch.empty(uor.suggested_scratch_i8(m, k, n), dtype=torch.uint8, device=dev)
+    if "cpu" in args.parts:
+        CPU_INPUTS["deep"] = True  # the CPU leg builds its own k-sample (A = B = -128)
     stream = torch.cuda.current_stream()
     route = {}
 
@@ -835,7 +837,7 @@ def cpu_baseline_i8(host, oracle):
         oracle.fast_gemm_i8_i32(N, N, N, 3, a, LD, b, LD, -1, c, LD, row0=0, rows=rows,
                                 threads=threads)
 
-    dt = median_time(run, runs=3)
+    dt = median_time(run, runs=5)
     rows1 = 256
     c1 = c0.copy()
     t0 = time.perf_counter()
@@ -853,7 +855,7 @@ def cpu_baseline_i8(host, oracle):
         "cores": threads,
         "kind": "port",
         "sample": f"rows 0..{rows} of the 8192^3 gemm_ex (alpha=3, beta=-1), median {dt:.2f} s "
-                  f"of 3 runs on {threads} threads, {'AVX-512 VNNI dpbusd' if vnni else 'AVX2'} "
+                  f"of 5 runs on {threads} threads, {'AVX-512 VNNI dpbusd' if vnni else 'AVX2'} "
                   "8x16 tile; rows are independent so TOPS scale to the full problem",
         "one_core": {"value": round(2.0 * rows1 * N * N / dt1 / 1e12, 4), "unit": "TOPS",
                      "sample": f"rows 0..{rows1}, {dt1:.2f} s (B packed once)"},
@@ -870,6 +872,8 @@ def cpu_baselines_secondary(oracle):
         groups on one core (extrapolated x 8);
       max-plus: the AVX2_TROP_I16 tile, all 4096 rows on all
         cores, 256 rows on one core (extrapolated);
+      deep case (configs[1] 2b): the chunked route on a k-sample, extrapolated,
+        every output checked against the closed form;
       exact float: the oracle's per-product exact register on a
         64-row slab on all cores (extrapolated to the full problem), 8 rows on
         one core."""
@@ -908,7 +912,7 @@ def cpu_baselines_secondary(oracle):
         N = trop["N"]
         c = np.full(N * N * 8, 0xEE, np.uint8)
         dt = median_time(lambda: oracle.fast_trop_i8(N, N, N, trop["a"], trop["b"], c,
-                                                    threads=threads), runs=3)
+                                                    threads=threads), runs=5)
         g, w = c.reshape(-1, 8), trop["c"].reshape(-1, 8)
         ok = bool(np.array_equal(g[:, :5], w[:, :5]))
         c1 = np.full(N * N * 8, 0xEE, np.uint8)
@@ -920,6 +924,32 @@ def cpu_baselines_secondary(oracle):
                        "sample": "the whole 4096^3 product", "bytes_equal_gpu": ok,
                        "one_core": {"value": round(rows1 * float(N) ** 2 / dt1 / 1e12, 4),
                                     "sample": f"rows 0..{rows1}, B packing included"}}
+    # Deep case (configs[1] 2b): m = n = 128, A = B = -128, the chunked route
+    # on a k-sample of 2^21 of the 2^24 (k-chunks are independent sums),
+    # extrapolated x 8; every output must be ksample * 2^14.
+    if CPU_INPUTS.get("deep"):
+        M, KS, KFULL = 128, 1 << 21, 1 << 24
+        a = np.full(M * KS, -128, np.int8)
+        c = np.zeros(M * M, np.int64)
+
+        def deep(th, kk):
+            c[:] = 7
+            oracle.fast_gemm_i8_i64_chunked(M, kk, M, a, kk, a, M, c, M, threads=th)
+
+        dt = median_time(lambda: deep(threads, KS), runs=5)
+        ok = bool((c == KS * 16384).all())
+        dt1 = median_time(lambda: deep(1, KS // 4), runs=1)
+        ok = ok and bool((c == (KS // 4) * 16384).all())
+        full_s = dt * KFULL / KS
+        out["deep"] = {"value": round(2.0 * M * M * KFULL / full_s / 1e12, 4), "unit": "TOPS",
+                       "GB_s": round(2.0 * M * KFULL / full_s / 1e9, 2), "cores": threads,
+                       "kind": "port",
+                       "sample": f"k = 2^21 of 2^24 (A = B = -128) in {dt * 1e3:.1f} ms, median of 5, "
+                                 "extrapolated x 8 (k-chunks are independent sums)",
+                       "outputs_equal_closed_form": ok,
+                       "one_core": {"value": round(2.0 * M * M * (KS // 4) / dt1 / 1e12, 4),
+                                    "sample": f"k = 2^19 in {dt1 * 1e3:.1f} ms"}}
+        del a
     for fl in CPU_INPUTS.get("float", []):
         N, is64 = fl["N"], fl["is64"]
         ft = np.float64 if is64 else np.float32
@@ -932,10 +962,14 @@ def cpu_baselines_secondary(oracle):
 
         c = np.full(rows * N, np.nan, ft)
         cuts = [rows * t // threads for t in range(threads + 1)]
-        t0 = time.perf_counter()
-        with ThreadPoolExecutor(threads) as pool:
-            sts = list(pool.map(lambda t: slab(cuts[t], cuts[t + 1], c), range(threads)))
-        dt = time.perf_counter() - t0
+        sts = []
+
+        def run_slab():
+            c[:] = np.nan
+            with ThreadPoolExecutor(threads) as pool:
+                sts[:] = list(pool.map(lambda t: slab(cuts[t], cuts[t + 1], c), range(threads)))
+
+        dt = median_time(run_slab, runs=3)
         ok = all(st == "ok" for st in sts) and bool(np.array_equal(
             c.view(np.uint64 if is64 else np.uint32), fl["c"].view(np.uint64 if is64 else np.uint32)))
         rows1 = 8
@@ -948,7 +982,7 @@ def cpu_baselines_secondary(oracle):
             "format": "f64" if is64 else "f32", "m": N, "n": N, "k": N,
             "value": round(2.0 * N ** 3 / full_s / 1e9, 3), "unit": "exact GFLOP/s",
             "cores": threads, "kind": "port",
-            "sample": f"rows 0..{rows} in {dt:.2f} s, extrapolated x{N // rows} "
+            "sample": f"rows 0..{rows} in {dt:.2f} s (median of 3), extrapolated x{N // rows} "
                       "(rows are independent)",
             "full_problem_s_extrapolated": round(full_s, 1),
             "ns_per_product_per_core": round(dt * threads / (rows * N * N) * 1e9, 2),

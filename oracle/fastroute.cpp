@@ -13,6 +13,8 @@
 //               x86.rs:704-715, 843-897); the AVX2 madd tile when VNNI is
 //               absent (x86.rs:80-96).  Exact i32 lanes fold to i128, then the
 //               Linear epilogue and the saturating i32 encode.
+//   fr_gemm_i8_i64_chunked -- the same tiles past one i32 lane: k streamed in
+//               65536-deep chunks folded into i64 (kernel.rs:1310-1376).
 //   fr_lut4        -- the table-lookup product over Packed<Grid<16>,2> codes,
 //               one call per codebook group as the decode-shape case makes
 //               them.  mode 0, tabulation (tabulated.rs:3867-4555 row_tile):
@@ -291,6 +293,38 @@ int fr_gemm_i8_i32(int m, int k, int n, int64_t alpha, const int8_t *a, int64_t 
     for (int t = 1; t < threads; ++t) pool.emplace_back(worker);
     worker();
     for (auto &t : pool) t.join();
+    return 0;
+}
+
+// The chunked full-depth route (kernel.rs:1310-1376) for depths past one i32
+// lane: C (m x n, i64, alpha 1, beta 0) += the exact sums over k, each 8 x 16
+// output tile streaming k in chunks of 65536 (|a|, |b| <= 128 keeps a chunk's
+// i32 lanes exact) folded into i64.  Output tiles are the work items (the
+// caller-driven partition).  Rows of A and B are k bytes apart (lda, ldb).
+int fr_gemm_i8_i64_chunked(int m, int64_t k, int n, const int8_t *a, int64_t lda, const int8_t *b,
+                           int64_t ldb, int64_t *c, int64_t ldc, int threads) {
+    constexpr int64_t KC = 65536;
+    if (threads < 1 || k % 4 != 0) return 4;
+    const bool vnni = have_vnni();
+    const int tm = (m + VMR - 1) / VMR, tn = (n + VNR - 1) / VNR;
+    parallel_items(tm * tn, threads, [&]() {
+        return [&, pa = std::vector<int8_t>((size_t)KC * VMR), pb = std::vector<int8_t>((size_t)KC * VNR)](
+                   int it) mutable {
+            const int i0 = it / tn * VMR, j0 = it % tn * VNR;
+            int64_t sum[VMR * VNR] = {0};
+            int32_t acc[VMR * VNR];
+            for (int64_t k0 = 0; k0 < k; k0 += KC) {
+                const int kc = (int)std::min<int64_t>(KC, k - k0);
+                pack_a_panel(a + k0, lda, kc, i0, m, pa.data());
+                pack_b_panel(b + k0 * ldb, ldb, kc, j0, n, pb.data());
+                if (vnni) tile_vnni(kc / 4, pa.data(), pb.data(), acc);
+                else tile_avx2(kc / 4, pa.data(), pb.data(), acc);
+                for (int e = 0; e < VMR * VNR; ++e) sum[e] += acc[e];
+            }
+            for (int i = 0; i < VMR && i0 + i < m; ++i)
+                for (int j = 0; j < VNR && j0 + j < n; ++j) c[(int64_t)(i0 + i) * ldc + j0 + j] = sum[i * VNR + j];
+        };
+    });
     return 0;
 }
 

@@ -199,6 +199,9 @@ def fast():
         F.fr_lut4.restype = _i32
         F.fr_trop_i8.argtypes = [_i32, _i32, _i32, _vp, _vp, _vp, _i32, _i32, _i32]
         F.fr_trop_i8.restype = _i32
+        F.fr_gemm_i8_i64_chunked.argtypes = [_i32, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _i64,
+                                             _i32]
+        F.fr_gemm_i8_i64_chunked.restype = _i32
         _fast = F
     return _fast
 
@@ -217,6 +220,12 @@ def fast_lut4(m, k, n, a, codes, books, group, c, groups=None, threads=1, mode="
     groups = n // group if groups is None else groups
     return fast().fr_lut4(m, k, n, _ptr(a), k, _ptr(codes), _ptr(books), group, _ptr(c), n,
                           groups, threads, {"tabulate": 0, "decode_dense": 1}[mode])
+
+
+def fast_gemm_i8_i64_chunked(m, k, n, a, lda, b, ldb, c, ldc, threads=1):
+    """The chunked route on the CPU baseline: C (int64) := A B over any depth."""
+    return fast().fr_gemm_i8_i64_chunked(m, k, n, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc,
+                                         threads)
 
 
 def fast_trop_i8(m, k, n, a, b, c, row0=0, rows=None, threads=1):

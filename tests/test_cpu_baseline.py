@@ -80,3 +80,20 @@ def test_fastroute_trop_matches_oracle(oracle, shape):
     g, w = got.reshape(-1, 8), want.reshape(-1, 8)
     assert np.array_equal(g[:, :5], w[:, :5])
     assert not w[:, 4].all() and w[:, 4].any()
+
+
+def test_fastroute_chunked_depth_matches_oracle(oracle):
+    """Past one i32 lane (three 65536-deep chunks and a ragged one), extremes
+    planted: every term -128 * -128 in row 0 / column 0."""
+    m, k, n = 9, 3 * 65536 + 256, 20
+    rng = np.random.default_rng(17)
+    a = rng.integers(-128, 128, m * k).astype(np.int8)
+    b = rng.integers(-128, 128, k * n).astype(np.int8)
+    a[:k] = -128
+    b.reshape(k, n)[:, 0] = -128
+    want = np.zeros(m * n, np.int64)
+    assert oracle.gemm_int(a, (m, k), (k, 1), b, (k, n), (n, 1), want, (m, n), (n, 1)) == "ok"
+    assert want[0] == k * 128 * 128
+    got = np.full(m * n, 7, np.int64)
+    assert oracle.fast_gemm_i8_i64_chunked(m, k, n, a, k, b, n, got, n, threads=3) == 0
+    assert np.array_equal(got, want)
