@@ -403,6 +403,46 @@ def test_tile256_column_major_b(uor, dev, m, n, k, out):
     assert np.array_equal(got[:, n:], c0.reshape(m, ldc)[:, n:])
 
 
+@pytest.mark.parametrize("m,k,n", [(512 + 24, 2048, 2048 + 16), (256, 4096 + 64, 4096), (1024, 1024, 1024),
+                                   (130, 64, 3008)])
+@pytest.mark.parametrize("out", ["i8", "i32", "i64", "i128"])
+def test_tile128_below_one_round(oracle, uor, dev, m, k, n, out):
+    """Fewer than 32 tiles of 256: the 128-wide direct-to-LDS tile with the
+    fused epilogue, ragged m and n, alpha = -3, beta = 2, every output width
+    (i128 through the parked full evaluation).  Rows 0, 1, the last two and a
+    middle one against the oracle, the rest against an exact float64 product."""
+    rng = np.random.default_rng(m + 3 * k + 7 * n)
+    lda, ldb, ldc = k + 16, n + 16, n + 4
+    a = rng.integers(-128, 128, m * lda).astype(np.int8)
+    b = rng.integers(-128, 128, k * ldb).astype(np.int8)
+    ob = {"i8": 1, "i32": 4, "i64": 8, "i128": 16}[out]
+    rec = 2 if out == "i128" else 1
+    dt = {1: np.int8, 4: np.int32, 8: np.int64, 16: np.int64}[ob]
+    info = np.iinfo(dt)
+    c0 = rng.integers(max(info.min, -(1 << 40)), min(info.max, 1 << 40), m * ldc * rec, dtype=dt)
+    gc = to_dev(c0, dev)
+    st, route = uor.gemm_i8(to_dev(a, dev), (m, k), (lda, 1), to_dev(b, dev), (k, n), (ldb, 1), gc,
+                            (m, n), (ldc, 1), out=out, alpha=-3, beta=2, encode="saturating")
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == 128, route
+    got = gc.cpu().numpy()
+    rows = sorted({0, 1, m // 2, m - 2, m - 1})
+    for r in rows:
+        want = c0.copy()
+        sub_c = want[r * ldc * rec:(r * ldc + n) * rec].copy()
+        assert oracle.gemm_int(a[r * lda:r * lda + k].copy(), (1, k), (k, 1), b, (k, n), (ldb, 1),
+                               sub_c, (1, n), (1, 1), alpha=-3, beta=2, encode="saturating",
+                               out_bytes=ob) == "ok"
+        assert np.array_equal(got[r * ldc * rec:(r * ldc + n) * rec], sub_c), (r, route)
+    if out in ("i32", "i64"):
+        S = a.reshape(m, lda)[:, :k].astype(np.float64) @ b.reshape(k, ldb)[:, :n].astype(np.float64)
+        want = np.clip(-3 * S.astype(np.int64) + 2 * c0.reshape(m, ldc)[:, :n].astype(np.int64),
+                       info.min, info.max)
+        assert np.array_equal(got.reshape(m, ldc)[:, :n].astype(np.int64), want)
+    # the padding columns are untouched
+    assert np.array_equal(got.reshape(m, ldc * rec)[:, n * rec:], c0.reshape(m, ldc * rec)[:, n * rec:])
+
+
 @pytest.mark.parametrize("m,k,n", [(128, 8192 + 64, 128), (200, 2 * 65536 + 192, 144),
                                    (64, 262144 + 64, 48)])
 def test_splitk_interleaved_steps(uor, dev, m, k, n):

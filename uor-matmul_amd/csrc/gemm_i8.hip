@@ -1300,6 +1300,14 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
         // registers; those requests take the 128-wide tile below.)
         bm = 256;
         if constexpr (FAST) UOR_HIP((launch_modes<256, 256, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
+    } else if (dl_ok(pair, K, N) && M >= 128) {
+        // Below one round of 256-wide tiles: the 128-wide direct-to-LDS tile
+        // (measured 21.3 against 25.9 us at 512 x 2048 x 2048, 32.2 against
+        // 46.0 us at 256 x 4096 x 4096 for the generic 64-wide tile; even at
+        // 1024^3, 16.4 us, where every tile choice takes the same time).
+        bm = 128;
+        UOR_HIP((launch_dl<128, 128, 2, 2, EPI_FUSED, FAST>(A, B, out, K, 0, 1, s)));
+        if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline
     } else if (t128 >= 192) {
         bm = 128;
         UOR_HIP((launch_modes<128, 128, 64, EPI_FUSED, FAST>(pair, A, B, out, K, 0, 1, s)));
