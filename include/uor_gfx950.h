@@ -512,7 +512,8 @@ typedef struct uor_tile {
 
 /* Partition::new + len (crates/uor-matmul-gemm/src/partition.rs:44-66): the
  * number of tiles of at most tile_rows x tile_cols covering an m x n output;
- * a zero tile extent means the whole extent.  0 exactly when m or n is 0. */
+ * a zero tile extent means the whole extent.  0 exactly when m or n is 0;
+ * UINT64_MAX when the count does not fit 64 bits. */
 uint64_t uor_gfx950_partition_len(uint64_t m, uint64_t n, uint64_t tile_rows,
                                   uint64_t tile_cols);
 

@@ -49,6 +49,11 @@ def test_partition_len_and_order(U):
     assert U.partition_len(0, 5, 2, 2) == 0 and U.partition_len(5, 0, 2, 2) == 0
     assert U.partition_len(5, 5, 0, 0) == 1
     assert U.partition_tile(5, 5, 0, 0, 0) == (0, 0, 5, 5)
+    # A count past 64 bits saturates, and every index below it still names
+    # its tile: (2^64 - 2) = (2^24 - 1) * 2^40 + (2^40 - 2).
+    big = 1 << 40
+    assert U.partition_len(big, big, 1, 1) == (1 << 64) - 1
+    assert U.partition_tile(big, big, 1, 1, (1 << 64) - 2) == ((1 << 24) - 1, big - 2, 1, 1)
 
 
 def window(rows, cols, rs, cs):

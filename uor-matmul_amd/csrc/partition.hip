@@ -102,16 +102,18 @@ int run_tiled(Family f, const uor_view *a, const uor_view *b, const uor_view *c,
 extern "C" uint64_t uor_gfx950_partition_len(uint64_t m, uint64_t n, uint64_t tile_rows,
                                              uint64_t tile_cols) {
     tile_extents(m, n, &tile_rows, &tile_cols);
-    return div_ceil(m, tile_rows) * div_ceil(n, tile_cols);
+    uint64_t len;
+    if (__builtin_mul_overflow(div_ceil(m, tile_rows), div_ceil(n, tile_cols), &len)) return UINT64_MAX;
+    return len;
 }
 
 // Partition::tile (partition.rs:83-98): tile `index` in row-major tile order,
 // clipped at the last row and column; 0 (None) past the end.
 extern "C" int uor_gfx950_partition_tile(uint64_t m, uint64_t n, uint64_t tile_rows,
                                          uint64_t tile_cols, uint64_t index, uor_tile *out) {
+    if (!out || index >= uor_gfx950_partition_len(m, n, tile_rows, tile_cols)) return 0;
     tile_extents(m, n, &tile_rows, &tile_cols);
     const uint64_t per_row = div_ceil(n, tile_cols);
-    if (!out || index >= div_ceil(m, tile_rows) * per_row) return 0;
     const uint64_t row = index / per_row * tile_rows, col = index % per_row * tile_cols;
     out->row = row;
     out->col = col;
