@@ -229,6 +229,8 @@ def lut_kernel_name(route):
     """The LUT kernel a route record names (uor_gfx950_gemm_lut4's choices)."""
     if route.get("kind") == "lut4_dot4":
         return "lut4_dot4_pf_kernel"
+    if route.get("split_k") == 16 and route.get("tile_n") == 8:
+        return "lut4_tile8_kernel"
     return {1: "lut4_lds_kernel", 4: "lut4_mfma16_kernel", 8: "lut4_tile_kernel", 16: "lut4_tile_kernel"}.get(
         route.get("split_k"), "lut4_mfma_kernel")
 

@@ -90,28 +90,31 @@ def test_lds_and_tile_kernel_epilogue(oracle, uor, dev, out, encode, k):
         assert (route["split_k"] in TILE) == (k <= 8192), route
 
 
-@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 32])
+@pytest.mark.parametrize("m", [1, 2, 5, 7, 8, 9, 16, 17, 32])
 @pytest.mark.parametrize("k", [2048, 4096, 6144, 8192])
 def test_tile_kernel_against_oracle(oracle, uor, dev, m, k):
-    """The 16-column tile kernel (one or two row blocks) at every depth it takes: ragged
-    n (a last tile of 3 columns), codebook groups that are not a multiple of
-    the 16-column tile (7) or are single columns, alpha/beta and the i64
-    epilogue, against the oracle."""
+    """The tile kernels at every depth they take: 8-column tiles at one row,
+    16-column tiles (one or two row blocks) beyond; ragged n (a last
+    tile of 3 or 2 columns), codebook groups that are not a multiple of the
+    tile (7) or are single columns, alpha/beta and the i64 epilogue, against
+    the oracle."""
     for n, group, out, alpha, beta in [(35, 7, np.int32, 1, 0), (50, 1, np.int64, -3, 2),
                                        (64, 128, np.int32, 5, -1)]:
         route = run_case(oracle, uor, dev, m, k, n, group, seed=m * 31 + k + n, out=out,
                          alpha=alpha, beta=beta)
         assert route["kind"] == "lut4_mfma" and route["split_k"] in TILE, route
+        assert route["tile_n"] == (8 if m == 1 else 16), route
 
 
 @pytest.mark.parametrize("m,k,n,group", [(1, 8192, 28672, 128), (8, 8192, 40000 + 9, 64),
                                          (32, 8192, 28672, 128), (24, 4096, 12 * 256 * 16, 128),
                                          (3, 2048, 16 * 100 + 1, 16), (12, 8192, 256 * 16, 3),
-                                         (16, 4096, 12 * 256 * 16 + 16, 128)])
+                                         (16, 4096, 12 * 256 * 16 + 16, 128),
+                                         (1, 4096, 12 * 512 * 8, 128), (1, 2048, 12 * 512 * 8 + 8, 128)])
 def test_tile_kernel_tiles_per_workgroup(uor, dev, m, k, n, group):
-    """The tile kernel with 7, 10 and 12 tiles per workgroup (the most whose
-    sums it holds), fewer tiles than CUs, one tile per CU, and one tile past
-    its limit (another kernel then); against a decode in torch plus a float64
+    """The tile kernels with 7, 10 and 12 tiles per workgroup (the most whose
+    sums they hold), fewer tiles than CUs, one tile per CU, and one tile past
+    the limit (another kernel then); against a decode in torch plus a float64
     matmul (exact: every sum is an integer below 2^53)."""
     rng = np.random.default_rng(m + k + n)
     a = to_dev(rng.integers(-128, 128, m * k).astype(np.int8), dev)
@@ -121,9 +124,12 @@ def test_tile_kernel_tiles_per_workgroup(uor, dev, m, k, n, group):
     st, route = uor.gemm_lut4(a, m, k, (k, 1), codes, n, books, group, c, (n, 1))
     torch.cuda.synchronize()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    tiled = (n + 15) // 16 <= 12 * cus
-    assert st == 0 and route["kind"] == "lut4_mfma", route
+    tiled8 = m == 1 and (n + 7) // 8 <= 12 * 2 * cus
+    tiled = tiled8 or (n + 15) // 16 <= 12 * cus
+    assert st == 0 and route["kind"] == ("lut4_mfma" if tiled or m > 4 else "lut4_dot4"), route
     assert (route["split_k"] in TILE) == tiled, route
+    if tiled:
+        assert route["tile_n"] == (8 if tiled8 else 16), route
     W = decode_torch(codes, n, k, books, group).to(torch.float64)
     want = a.view(m, k).to(torch.float64) @ W.T
     assert torch.equal(c.view(m, n).to(torch.float64), want), route

@@ -50,7 +50,29 @@ struct LutArgs {
     int64_t alpha, beta;
     int mode;
     uint32_t sel_mask, sel_base;  // 0x04040404, 0x03020100 (kernel arguments, so they live in SGPRs)
+    // j / group for 32-bit j as ((hi(j * gm) + ((j - hi) >> gs1)) >> gs2)
+    // (Granlund & Montgomery, division by invariant integers, fig. 4.1),
+    // set by lut_group_magic; the tile kernels use it for their codebook rows.
+    uint32_t gm, gs1, gs2;
 };
+
+// The magic numbers of LutArgs for a divisor d (1 <= d < 2^32): with
+// l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, s1 = min(l, 1),
+// s2 = max(l - 1, 0), exact for every 32-bit dividend.
+static void lut_group_magic(LutArgs &L, uint64_t d) {
+    if (d > 0x80000000ull) d = 0x80000000ull;  // the tile kernels' columns are far below 2^31
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    L.gm = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    L.gs1 = l < 1 ? l : 1;
+    L.gs2 = l > 0 ? l - 1 : 0;
+}
+
+// Column j's codebook row, j < 2^32.
+__device__ inline uint32_t lut_group_of(uint32_t j, uint32_t gm, uint32_t gs1, uint32_t gs2) {
+    const uint32_t t = __umulhi(j, gm);
+    return (t + ((j - t) >> gs1)) >> gs2;
+}
 
 __device__ inline uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
     return __builtin_amdgcn_perm(s0, s1, sel);
@@ -394,15 +416,23 @@ static bool lut_tile_on() {
     }();
     return on;
 }
-// Waves per workgroup of the tile kernel (UOR_GFX950_LUT_TILE=8 or 16, for
-// measurement; 16, the default, measured 23.3 against 24.7 us at m = 1 and
-// the config weights).
+// Waves per workgroup of the 16-column tile kernel (UOR_GFX950_LUT_TILE=8 or
+// 16, for measurement; 16, the default, measured 23.3 against 24.7 us at
+// m = 1 and the config weights).  Either value also turns the 8-column
+// kernel off, so the 16-column one runs at every m it takes.
 static int lut_tile_waves() {
     static int w = [] {
         const char *e = getenv("UOR_GFX950_LUT_TILE");
         return (e && !strcmp(e, "8")) ? 8 : 16;
     }();
     return w;
+}
+static bool lut_tile8_on() {
+    static bool on = [] {
+        const char *e = getenv("UOR_GFX950_LUT_TILE");
+        return !(e && (!strcmp(e, "8") || !strcmp(e, "16")));
+    }();
+    return on;
 }
 
 static int lut_variant() {
@@ -848,9 +878,9 @@ __device__ inline void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Finish the batch of tiles [t0, t0 + cnt) of workgroup b (tiles b + G*i)
-// from the tile sums in LDS: 4 consecutive columns per item.
-template <int ROWS, int TSW>
+// Finish the batch of tiles [t0, t0 + cnt) of workgroup b (tiles b + G*i,
+// TW columns each) from the tile sums in LDS: 4 consecutive columns per item.
+template <int ROWS, int TSW, int TW = 16>
 __device__ __attribute__((noinline)) void lut_tile_finish(char *cbase, int64_t crs, int64_t ccs, int ob, int64_t alpha,
                                                           int64_t beta, int mode, uint64_t m, uint64_t n,
                                                           const int *tsum, uint32_t b, uint32_t G, uint32_t t0,
@@ -864,10 +894,11 @@ __device__ __attribute__((noinline)) void lut_tile_finish(char *cbase, int64_t c
     L.beta = beta;
     L.mode = mode;
     const bool vec = ob == 4 && ccs == 1 && ((uintptr_t)cbase & 15) == 0 && (crs & 3) == 0 && alpha == 1 && beta == 0;
-    for (uint32_t e = threadIdx.x; e < cnt * ROWS * 4; e += blockDim.x) {
-        const uint32_t sl = e / (ROWS * 4), row = (e / 4) % ROWS, c4 = e % 4;
+    constexpr uint32_t Q = TW / 4;
+    for (uint32_t e = threadIdx.x; e < cnt * ROWS * Q; e += blockDim.x) {
+        const uint32_t sl = e / (ROWS * Q), row = (e / Q) % ROWS, c4 = e % Q;
         if (row >= m) continue;
-        const uint64_t col0 = (uint64_t)(b + G * (t0 + sl)) * 16 + 4 * c4;
+        const uint64_t col0 = (uint64_t)(b + G * (t0 + sl)) * TW + 4 * c4;
         const int *ts = &tsum[(sl * ROWS + row) * TSW + 4 * c4];
         if (vec && col0 + 4 <= n) {
             *(v4i *)((int32_t *)cbase + (int64_t)row * crs + (int64_t)col0) = v4i{ts[0], ts[1], ts[2], ts[3]};
@@ -899,32 +930,19 @@ __global__ void __launch_bounds__(64 * W) lut4_tile_kernel(LutArgs L, uint32_t n
     const uint32_t ntl = b < ntiles ? (ntiles - 1 - b) / G + 1 : 0;  // this workgroup's tiles
     if (ntl == 0) return;
     const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
-    const uint64_t n = L.n, m = L.m, half = L.half, group = L.group;
+    const uint64_t n = L.n, m = L.m, half = L.half;
+    const uint32_t n32 = (uint32_t)n, gm = __builtin_amdgcn_readfirstlane(L.gm),
+                   gs1 = __builtin_amdgcn_readfirstlane(L.gs1), gs2 = __builtin_amdgcn_readfirstlane(L.gs2);
     const uint8_t *const codes = L.codes;
     const int8_t *const books = L.books;
     const uint32_t tb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)tbuf;
 
-    // Activations in the decode's order: act[p][h][b] covers row 16b + c,
-    // weights w*k/W + 128p + 32g + 16h + [0, 16).  Rows past m read row m-1
-    // and are zeroed.
-    v4i act[NP][2][MB];
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int bb = 0; bb < MB; ++bb) {
-                const uint64_t r = 16 * bb + c < m ? 16 * bb + c : m - 1;
-                const uint64_t kk = (uint64_t)(128 * NP) * wave + 128 * p + 32 * g + 16 * h;
-                act[p][h][bb] = *(global_v4i_c *)(L.a + (int64_t)r * L.ars + (int64_t)kk);
-            }
     // Column c's codebook of tile i (16 bytes; a ragged tile's missing
     // columns read the last column's).
 #define UOR_LT_BOOK(I)                                                                         \
     ([&]() -> v4i {                                                                            \
-        uint64_t j_ = (uint64_t)(b + G * (I)) * 16 + c;                                        \
-        if (j_ >= n) j_ = n - 1;                                                               \
-        return *(global_v4i_c *)(books + (j_ / group) * 16);                                   \
+        const uint32_t j_ = min((b + G * (I)) * 16u + (uint32_t)c, n32 - 1);                   \
+        return *(global_v4i_c *)(books + (uint64_t)lut_group_of(j_, gm, gs1, gs2) * 16);        \
     }())
     // This wave's piece e of tile i: column CPW*w + e / KQ, bytes
     // [1024 * (e % KQ), +1024), lane l's 16 bytes at +16l (the wave's pieces
@@ -943,10 +961,31 @@ __global__ void __launch_bounds__(64 * W) lut4_tile_kernel(LutArgs L, uint32_t n
         lds_wr16((BUF) + cc_ * CB + 16u * ((64u * ((E) % KQ) + lane) ^ cc_), (V));             \
     }
 
+    // Activations in the decode's order: act[p][h][b] covers row 16b + c,
+    // weights w*k/W + 128p + 32g + 16h + [0, 16).  Rows past m read row m-1
+    // and are zeroed.
+    v4i act[NP][2][MB];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int bb = 0; bb < MB; ++bb) {
+                const uint64_t r = 16 * bb + c < m ? 16 * bb + c : m - 1;
+                const uint64_t kk = (uint64_t)(128 * NP) * wave + 128 * p + 32 * g + 16 * h;
+                act[p][h][bb] = *(global_v4i_c *)(L.a + (int64_t)r * L.ars + (int64_t)kk);
+            }
     v4i bk = UOR_LT_BOOK(0u);
-    v4i ring[PW];
+    // Tiles 0 and 1 are requested together, after the activations and the
+    // first codebook (the loads complete in order, so whatever waits for
+    // those does not wait for the codes): tile 1 is in flight while tile 0
+    // is stored.  A workgroup with one tile reads tile 0 twice, the second
+    // time from the cache.
+    v4i ring[PW], ring1[PW];
 #pragma unroll
     for (int e = 0; e < PW; ++e) ring[e] = ld_nt16(UOR_LT_PIECE(0u, e));
+#pragma unroll
+    for (int e = 0; e < PW; ++e) ring1[e] = ld_nt16(UOR_LT_PIECE(ntl > 1 ? 1u : 0u, e));
     for (int e = threadIdx.x; e < LT_NTB * ROWS * TSW; e += NT) tsum[e] = 0;
     // Activations into the decode's order (rows past m zero).
 #pragma unroll
@@ -960,11 +999,11 @@ __global__ void __launch_bounds__(64 * W) lut4_tile_kernel(LutArgs L, uint32_t n
                 act[p][h][bb] = v4i{(int)perm(x[1], x[0], 0x06040200u), (int)perm(x[1], x[0], 0x07050301u),
                                     (int)perm(x[3], x[2], 0x06040200u), (int)perm(x[3], x[2], 0x07050301u)};
             }
-    // Tile 0 into its buffer, tile 1 requested.
+    // Tile 0 into its buffer; tile 1 stays in flight.
 #pragma unroll
     for (int e = 0; e < PW; ++e) {
         UOR_LT_STORE(tb0, e, ring[e])
-        if (ntl > 1) ring[e] = ld_nt16(UOR_LT_PIECE(1u, e));
+        ring[e] = ring1[e];
     }
     lds_barrier();
 
@@ -1033,6 +1072,170 @@ __global__ void __launch_bounds__(64 * W) lut4_tile_kernel(LutArgs L, uint32_t n
 #undef UOR_LT_STORE
 #undef UOR_LT_PIECE
 #undef UOR_LT_BOOK
+}
+
+// ------------------------------ m = 1 (up to 8): 8-column tiles, two per CU
+//
+// The same code stream at half the tile: one workgroup of 8 waves owns the
+// 8-column tiles t = b, b + G, ... (32 KiB at k = 8192; G = two workgroups
+// per CU), wave w loads column w of the next tile, one tile in flight, one
+// barrier per tile.  Two workgroups per CU, each on its own barrier, kept
+// the code stream at 6.4 TB/s where one 16-column workgroup per CU ran at
+// 6.0 (the same loads with no compute, MI355X), and a workgroup's last tile
+// is half the decode.
+//
+// The MFMA still takes 16 rows: with at most 8 activation rows, rows 0-7 of
+// the A operand carry the tile's 8 columns over the first half of a wave's
+// weights and rows 8-15 the same columns over the second half; the B
+// operand's columns 0-7 and 8-15 carry the activation rows over the same two
+// halves.  The two diagonal 8x8 blocks of the result are then the two
+// halves' sums (the off-diagonal blocks pair different weights and are
+// dropped), and both are added into the tile sums.
+//
+// Lane (c = l%16, g = l/16) works on virtual column c: tile column c%8, half
+// r = c/8.  Wave w' takes weights [w'*k/8, (w'+1)*k/8) of every column, half
+// r the r-th half of that; per pair p of its half it reads 16 code bytes
+// (weights 32g..+32 of the pair) and makes two A operands, as the 16-column
+// kernel does.  LDS: virtual column c holds its CB/2 bytes in chunk order,
+// chunk x of it at slot x ^ c, so a read phase (16 lanes, one chunk index)
+// hits 16 distinct slots; a wave's 1 KiB piece scatters over the two halves
+// it spans.
+template <int KQ>
+__global__ void __launch_bounds__(512) lut4_tile8_kernel(LutArgs L, uint32_t ntiles) {
+    constexpr int TSW = 9;           // words per tile-sum row (8 columns + pad)
+    constexpr int CB = KQ * 1024;    // code bytes per column (k / 2)
+    constexpr int VB = CB / 2;       // bytes per virtual column
+    constexpr int TB = 8 * CB;       // code bytes per tile
+    constexpr int HC = 4 * KQ;       // chunks per half of a wave's range
+    constexpr int NP = KQ;           // pairs per half
+    __shared__ __attribute__((aligned(16))) uint8_t tbuf[2 * TB];
+    __shared__ int tsum[LT_NTB * 8 * TSW];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int cc = c & 7, r = c >> 3;
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t ntl = b < ntiles ? (ntiles - 1 - b) / G + 1 : 0;
+    if (ntl == 0) return;
+    const uint32_t m4 = __builtin_amdgcn_readfirstlane(L.sel_mask), id = __builtin_amdgcn_readfirstlane(L.sel_base);
+    const uint64_t n = L.n, m = L.m, half = L.half;
+    const uint32_t n32 = (uint32_t)n, gm = __builtin_amdgcn_readfirstlane(L.gm),
+                   gs1 = __builtin_amdgcn_readfirstlane(L.gs1), gs2 = __builtin_amdgcn_readfirstlane(L.gs2);
+    const uint8_t *const codes = L.codes;
+    const int8_t *const books = L.books;
+    const uint32_t tb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)tbuf;
+
+    // Activations: act[p][h] covers row cc, weights
+    // 128 * (2KQ*w + KQ*r + p) + 32g + 16h + [0, 16).  Rows past m read row
+    // m-1 and are zeroed.
+    v4i act[NP][2];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint64_t row = (uint64_t)cc < m ? (uint64_t)cc : m - 1;
+            const uint64_t kk = (uint64_t)128 * (2 * KQ * wave + KQ * r + p) + 32 * g + 16 * h;
+            act[p][h] = *(global_v4i_c *)(L.a + (int64_t)row * L.ars + (int64_t)kk);
+        }
+#define UOR_LT8_BOOK(I)                                                                        \
+    ([&]() -> v4i {                                                                            \
+        const uint32_t j_ = min((b + G * (I)) * 8u + (uint32_t)cc, n32 - 1);                   \
+        return *(global_v4i_c *)(books + (uint64_t)lut_group_of(j_, gm, gs1, gs2) * 16);        \
+    }())
+    // Wave w's piece e of tile i: column w, bytes [1024e, +1024), lane l's
+    // 16 bytes at +16l.  A ragged last tile re-reads a valid row (never stored).
+#define UOR_LT8_PIECE(I, E)                                                                    \
+    ([&]() -> const uint8_t * {                                                               \
+        uint64_t j_ = (uint64_t)(b + G * (I)) * 8 + wave;                                      \
+        if (j_ >= n) j_ = n - 1;                                                               \
+        return codes + j_ * half + 1024 * (E) + 16 * lane;                                     \
+    }())
+    // Chunk x = 64e + l of column w: wave range x / (2HC), half (x / HC) & 1,
+    // place x % HC within it; virtual column w + 8 * half, chunk
+    // HC * range + place, at slot chunk ^ virtual column.
+#define UOR_LT8_STORE(BUF, E, V)                                                               \
+    {                                                                                          \
+        const uint32_t x_ = 64u * (E) + (uint32_t)lane;                                        \
+        const uint32_t vc_ = (uint32_t)wave + 8u * ((x_ / HC) & 1u);                           \
+        const uint32_t vx_ = HC * (x_ / (2 * HC)) + x_ % HC;                                   \
+        lds_wr16((BUF) + vc_ * VB + 16u * (vx_ ^ vc_), (V));                                   \
+    }
+
+    v4i bk = UOR_LT8_BOOK(0u);
+    v4i ring[KQ], ring1[KQ];
+#pragma unroll
+    for (int e = 0; e < KQ; ++e) ring[e] = ld_nt16(UOR_LT8_PIECE(0u, e));
+#pragma unroll
+    for (int e = 0; e < KQ; ++e) ring1[e] = ld_nt16(UOR_LT8_PIECE(ntl > 1 ? 1u : 0u, e));
+    for (int e = threadIdx.x; e < LT_NTB * 8 * TSW; e += 512) tsum[e] = 0;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v4i x = act[p][h];
+            if ((uint64_t)cc >= m) x = v4i{0, 0, 0, 0};
+            act[p][h] = v4i{(int)perm(x[1], x[0], 0x06040200u), (int)perm(x[1], x[0], 0x07050301u),
+                            (int)perm(x[3], x[2], 0x06040200u), (int)perm(x[3], x[2], 0x07050301u)};
+        }
+#pragma unroll
+    for (int e = 0; e < KQ; ++e) {
+        UOR_LT8_STORE(tb0, e, ring[e])
+        ring[e] = ring1[e];
+    }
+    lds_barrier();
+
+    // Lane l's share of a result: column 4(q&1) + i of the tile and activation
+    // row l%8 for q = l/16, valid on the diagonal blocks (q/2 == (l%16)/8).
+    const bool diag = (g >> 1) == r;
+#define UOR_LT8_ITER(I, NEXT, AFTER)                                                           \
+    {                                                                                          \
+        const uint32_t i_ = (I);                                                               \
+        const uint32_t cur = tb0 + (i_ & 1) * TB, nxt = tb0 + ((i_ + 1) & 1) * TB;             \
+        const uint32_t q0 = (uint32_t)bk[0], q1 = (uint32_t)bk[1], q2 = (uint32_t)bk[2],       \
+                       q3 = (uint32_t)bk[3];                                                   \
+        if (NEXT) bk = UOR_LT8_BOOK(i_ + 1);                                                   \
+        v4i cw[NP];                                                                            \
+        _Pragma("unroll") for (int p = 0; p < NP; ++p) {                                       \
+            const uint32_t x = (uint32_t)(HC * wave + 4 * p + g);                              \
+            cw[p] = lds_rd16_asm(cur + (uint32_t)c * VB + 16u * (x ^ (uint32_t)c));             \
+        }                                                                                      \
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                    \
+        _Pragma("unroll") for (int p = 0; p < NP; ++p) asm volatile("" : "+v"(cw[p]));          \
+        v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};                                       \
+        _Pragma("unroll") for (int p = 0; p < NP; ++p) {                                       \
+            _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                    \
+                uint32_t e0, o0, e1, o1;                                                       \
+                decode8((uint32_t)cw[p][2 * h], q0, q1, q2, q3, m4, id, e0, o0);               \
+                decode8((uint32_t)cw[p][2 * h + 1], q0, q1, q2, q3, m4, id, e1, o1);           \
+                const v4i wop = v4i{(int)e0, (int)o0, (int)e1, (int)o1};                       \
+                acc[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, act[p][h], acc[h], 0, 0, 0); \
+            }                                                                                  \
+        }                                                                                      \
+        if (diag && (uint64_t)cc < m) {                                                        \
+            _Pragma("unroll") for (int v = 0; v < 4; ++v)                                      \
+                atomicAdd(&tsum[(i_ * 8 + cc) * TSW + 4 * (g & 1) + v], acc[0][v] + acc[1][v]); \
+        }                                                                                      \
+        if (NEXT) {                                                                            \
+            _Pragma("unroll") for (int e = 0; e < KQ; ++e) {                                   \
+                UOR_LT8_STORE(nxt, e, ring[e])                                                 \
+                if (AFTER) ring[e] = ld_nt16(UOR_LT8_PIECE(i_ + 2, e));                        \
+            }                                                                                  \
+        }                                                                                      \
+        lds_barrier();                                                                         \
+    }
+    uint32_t i = 0;
+    for (; i + 2 < ntl; ++i) UOR_LT8_ITER(i, true, true)
+    if (i + 1 < ntl) {
+        UOR_LT8_ITER(i, true, false)
+        ++i;
+    }
+    UOR_LT8_ITER(i, false, false)
+    lut_tile_finish<8, TSW, 8>(L.c, L.crs, L.ccs, L.ob, L.alpha, L.beta, L.mode, m, n, tsum, b, G, 0, ntl);
+#undef UOR_LT8_ITER
+#undef UOR_LT8_STORE
+#undef UOR_LT8_PIECE
+#undef UOR_LT8_BOOK
 }
 
 // ------------------------------------------- many rows: decode, then dense
@@ -1124,7 +1327,8 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
     if (m == 0 || n == 0) return UOR_OK;
 
     LutArgs L{(const int8_t *)A.base, A.rs, A.cs, codes, k / 2, books, group, m, k, n,
-              C.base, C.rs, C.cs, out_type, alpha, beta, encode, 0x04040404u, 0x03020100u};
+              C.base, C.rs, C.cs, out_type, alpha, beta, encode, 0x04040404u, 0x03020100u, 0, 0, 0};
+    lut_group_magic(L, group);
     hipStream_t s = (hipStream_t)stream;
     // 16-byte code loads need 16-byte aligned rows; 8-byte activation loads
     // need a unit column stride and 8-byte aligned rows.
@@ -1170,6 +1374,25 @@ extern "C" int uor_gfx950_gemm_lut4(const uor_view *a, const uint8_t *codes, uin
         ((uintptr_t)books & 15) == 0 && lut_tile_on()) {
         const uint64_t ntiles = (n + 15) / 16;
         const uint64_t cus = (uint64_t)device_cus_lut();
+        // m = 1: the 8-column tiles, two workgroups per CU (measured at the
+        // config weights: m = 1 22.0-22.4 against 22.3-22.8 us for the
+        // 16-column tiles; from m = 2 on even, and 0.5-1.7 us slower at m = 8).
+        const uint64_t nt8 = (n + 7) / 8;
+        if (m == 1 && lut_tile8_on() && (nt8 + 2 * cus - 1) / (2 * cus) <= (uint64_t)LT_NTB) {
+            const unsigned G = (unsigned)std::min<uint64_t>(2 * cus, nt8);
+            if (route) route->tile_m = 8, route->tile_n = 8, route->tile_k = (int)(k / 16), route->split_k = 16,
+                       route->kind = UOR_ROUTE_LUT4_MFMA;
+#define UOR_LT8(KQ) hipLaunchKernelGGL((lut4_tile8_kernel<KQ>), dim3(G), dim3(512), 0, s, L, (uint32_t)nt8);
+            switch (k / 2048) {
+            case 1: UOR_LT8(1); break;
+            case 2: UOR_LT8(2); break;
+            case 3: UOR_LT8(3); break;
+            default: UOR_LT8(4); break;
+            }
+#undef UOR_LT8
+            UOR_HIP(hipGetLastError());
+            return UOR_OK;
+        }
         if ((ntiles + cus - 1) / cus <= (uint64_t)LT_NTB) {
             const unsigned G = (unsigned)std::min<uint64_t>(cus, ntiles);
             const int w = lut_tile_waves();
