@@ -778,10 +778,46 @@ def bench_config1(args, torch, uor, gen):
     ms = s0.elapsed_time(s1) / steps
     A = ga.view(n, n).to(torch.float64)
     B = gb.view(n, n).to(torch.float64)
-    parity = bool(torch.equal(gc.view(n, n).to(torch.float64), A @ B))
+    want = A @ B
+    parity = bool(torch.equal(gc.view(n, n).to(torch.float64), want))
+
+    # The same calls captured in a HIP graph (50 per graph, replayed): the
+    # device's time per call without the host's per-call cost (Python, ctypes
+    # and the launch), which bounds the eager loop above at this size.
+    per_graph = 50
+    gc.zero_()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        uor.slice_gemm_i8(n, n, n, ga, gb, gc, scratch=sc, stream=side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream().cuda_stream
+        for _ in range(per_graph):
+            if uor.slice_gemm_i8(n, n, n, ga, gb, gc, scratch=sc, stream=cs) != 0:
+                raise RuntimeError("slice::gemm status under capture")
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(4, steps // per_graph)
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    g1.record(stream)
+    torch.cuda.synchronize()
+    ms_graph = g0.elapsed_time(g1) / (replays * per_graph)
+    gc.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    parity = parity and bool(torch.equal(gc.view(n, n).to(torch.float64), want))
+    del graph
     return {"config": "BASELINE configs[0]: slice::gemm i8 -> i32, 1024^3, xorshift operands, "
                       "suggested offer", "m": n, "k": n, "n": n, "ms_per_call": round(ms, 5),
-            "TOPS": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1), "parity": parity}
+            "TOPS": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1),
+            "ms_per_call_graph": round(ms_graph, 5),
+            "TOPS_graph": round(2.0 * n ** 3 / (ms_graph * 1e-3) / 1e12, 1), "parity": parity}
 
 
 def cpu_threads():

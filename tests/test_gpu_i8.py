@@ -403,14 +403,10 @@ def test_tile256_column_major_b(uor, dev, m, n, k, out):
     assert np.array_equal(got[:, n:], c0.reshape(m, ldc)[:, n:])
 
 
-@pytest.mark.parametrize("m,k,n", [(512 + 24, 2048, 2048 + 16), (256, 4096 + 64, 4096), (1024, 1024, 1024),
-                                   (130, 64, 3008)])
-@pytest.mark.parametrize("out", ["i8", "i32", "i64", "i128"])
-def test_tile128_below_one_round(oracle, uor, dev, m, k, n, out):
-    """Fewer than 32 tiles of 256: the 128-wide direct-to-LDS tile with the
-    fused epilogue, ragged m and n, alpha = -3, beta = 2, every output width
-    (i128 through the parked full evaluation).  Rows 0, 1, the last two and a
-    middle one against the oracle, the rest against an exact float64 product."""
+def check_small_tile(oracle, uor, dev, m, k, n, out, tile):
+    """One call with ragged m and n, alpha = -3, beta = 2, saturating, on the
+    route with `tile`-wide tiles.  Rows 0, 1, the last two and a middle one
+    against the oracle, the rest against an exact float64 product."""
     rng = np.random.default_rng(m + 3 * k + 7 * n)
     lda, ldb, ldc = k + 16, n + 16, n + 4
     a = rng.integers(-128, 128, m * lda).astype(np.int8)
@@ -424,9 +420,10 @@ def test_tile128_below_one_round(oracle, uor, dev, m, k, n, out):
     st, route = uor.gemm_i8(to_dev(a, dev), (m, k), (lda, 1), to_dev(b, dev), (k, n), (ldb, 1), gc,
                             (m, n), (ldc, 1), out=out, alpha=-3, beta=2, encode="saturating")
     torch.cuda.synchronize()
-    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == 128, route
+    assert st == 0 and route["kind"] == "mfma_tile" and route["tile_m"] == tile, route
+    assert route["operand_modes"] & (1 << 4), route  # the direct-to-LDS pipeline
     got = gc.cpu().numpy()
-    rows = sorted({0, 1, m // 2, m - 2, m - 1})
+    rows = sorted({r for r in (0, 1, m // 2, m - 2, m - 1) if 0 <= r < m})
     for r in rows:
         want = c0.copy()
         sub_c = want[r * ldc * rec:(r * ldc + n) * rec].copy()
@@ -441,6 +438,28 @@ def test_tile128_below_one_round(oracle, uor, dev, m, k, n, out):
         assert np.array_equal(got.reshape(m, ldc)[:, :n].astype(np.int64), want)
     # the padding columns are untouched
     assert np.array_equal(got.reshape(m, ldc * rec)[:, n * rec:], c0.reshape(m, ldc * rec)[:, n * rec:])
+
+
+@pytest.mark.parametrize("m,k,n", [(512 + 24, 2048 + 64, 2048 + 16), (260, 4096 + 64, 3840),
+                                   (1024 + 64, 2048 + 128, 1024), (320, 2048 + 64, 3520)])
+@pytest.mark.parametrize("out", ["i8", "i32", "i64", "i128"])
+def test_tile128_below_one_round(oracle, uor, dev, m, k, n, out):
+    """Fewer than 32 tiles of 256, more 64-wide tiles than CUs and k > 2048:
+    the 128-wide direct-to-LDS tile with the fused epilogue, every output
+    width (i128 through the parked full evaluation)."""
+    check_small_tile(oracle, uor, dev, m, k, n, out, 128)
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (256, 4096 + 64, 4096), (130, 64, 3008), (64, 8192, 4096),
+                                   (1, 1024, 1024), (33, 192, 80), (200, 960, 1040), (16, 4096, 8192),
+                                   (40, 4160, 8208), (1000, 2048, 2000)])
+@pytest.mark.parametrize("out", ["i8", "i32", "i64", "i128"])
+def test_ring64_one_round(oracle, uor, dev, m, k, n, out):
+    """At most one 64-wide tile per CU (two at k <= 2048): the 64-wide
+    direct-to-LDS tile with sixteen stages in flight; reductions shorter than
+    the ring (1, 3 and 15 steps), as long as it (16), and longer (32, 64, 65,
+    128), ragged m and n, skinny products the 256-wide tile took before."""
+    check_small_tile(oracle, uor, dev, m, k, n, out, 64)
 
 
 @pytest.mark.parametrize("m,k,n", [(128, 8192 + 64, 128), (200, 2 * 65536 + 192, 144),
@@ -509,7 +528,7 @@ def test_splitk_narrow_tile_folds_segments(uor, dev):
 
 
 @pytest.mark.parametrize("m,k,n", [(512, 1024, 28672), (256, 2048, 28672), (300, 640, 20000),
-                                   (16, 4096, 8192), (40, 4160, 8208), (100, 4096, 9008)])
+                                   (16, 4096, 20480), (40, 4160, 16400), (100, 4096, 9008)])
 @pytest.mark.parametrize("out", ["i32", "i64"])
 def test_wide_tile_below_one_round(uor, dev, m, k, n, out):
     """Fewer 256-wide tiles than CUs, wide n (and from 16 rows at k >= 4096):

@@ -421,11 +421,12 @@ gemm_i8_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm,
 
 // WM x WN waves of 64 lanes (4 waves: one per SIMD, 128x128 each at BM=BN=256;
 // 8 waves: two per SIMD, so one wave's LDS reads overlap the other's MFMAs).
-template <int BM, int BN, int WM, int WN, int EPI, bool FAST, int OB, bool PF>
+// NS > 4: the k loop on a ring of NS stages (dl_mainloop_ring).
+template <int BM, int BN, int WM, int WN, int EPI, bool FAST, int OB, bool PF, int NS = DL_NSTAGE>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
 gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int gm, int gn) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
-    using L = DlLayout<BM, BN>;
+    using L = DlLayout<BM, BN, NS>;
     static_assert(WM * WN * (32 * 33) * 4 <= L::BYTES, "epilogue parking fits the stages");
     __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
     char *st0 = lds, *st1 = lds + L::A_BYTES, *st2 = lds + 2 * L::A_BYTES, *st3 = lds + 3 * L::A_BYTES;
@@ -462,7 +463,8 @@ gemm_i8_dl_kernel(Opnd A, Opnd B, OutArgs out, uint64_t K, uint64_t kslice, int 
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
-    if constexpr (PF) dl_mainloop_pf<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc, kstep);
+    if constexpr (NS != DL_NSTAGE) dl_mainloop_ring<BM, BN, WM, WN, NS>(A, B, m0, n0, kbeg, nk, lds, acc, kstep);
+    else if constexpr (PF) dl_mainloop_pf<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc, kstep);
     else dl_mainloop<BM, BN, WM, WN>(A, B, m0, n0, kbeg, nk, st0, st1, st2, st3, acc, kstep);
     __syncthreads();
 
@@ -1010,16 +1012,16 @@ static hipError_t launch_tile(const Opnd &A, const Opnd &B, const OutArgs &out, 
 }
 
 
-template <int BM, int BN, int WM, int WN, int EPI, bool FAST, bool PF = false>
+template <int BM, int BN, int WM, int WN, int EPI, bool FAST, bool PF = false, int NS = DL_NSTAGE>
 static hipError_t launch_dl(const Opnd &A, const Opnd &B, const OutArgs &out, uint64_t K,
                             uint64_t kslice, int splits, hipStream_t s) {
-    auto kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 4, PF>;
+    auto kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 4, PF, NS>;
     if constexpr (EPI != EPI_PARTIAL) {
         switch (out.ob) {
-        case 1: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 1, PF>; break;
-        case 2: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 2, PF>; break;
-        case 8: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 8, PF>; break;
-        case 16: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, false, 16, PF>; break;
+        case 1: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 1, PF, NS>; break;
+        case 2: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 2, PF, NS>; break;
+        case 8: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, FAST, 8, PF, NS>; break;
+        case 16: kern = gemm_i8_dl_kernel<BM, BN, WM, WN, EPI, false, 16, PF, NS>; break;
         default: break;
         }
     }
@@ -1027,6 +1029,17 @@ static hipError_t launch_dl(const Opnd &A, const Opnd &B, const OutArgs &out, ui
     dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
     hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), 0, s, A, B, out, K, kslice, gm, gn);
     return hipGetLastError();
+}
+
+static int device_cus();
+// The most 64-wide tiles the ring kernel takes (UOR_GFX950_RING64 overrides,
+// for measurement; 0 turns it off).
+static int ring64_tiles() {
+    static int t = [] {
+        const char *e = getenv("UOR_GFX950_RING64");
+        return e ? atoi(e) : device_cus();
+    }();
+    return t;
 }
 
 static int device_cus() {
@@ -1280,7 +1293,22 @@ static int run_i8(const Placed &PA, const Placed &PB, const Placed &PC, int ob, 
     // against 0.032 ms).
     const bool use256 = t256 >= 256 || (N >= 128 && t256 >= 32 && (M >= 128 || (M >= 16 && K >= 4096)));
     int bm;
-    if (use256 && pair == 1 && dl_variant() == DL_S4 && s4t_ok(A, B, K)) {
+    const uint64_t r64 = (uint64_t)ring64_tiles();
+    if (dl_ok(pair, K, N) && (t64 <= r64 || (t64 <= 2 * r64 && K <= 2048))) {
+        // At most one round of 64-wide tiles (two at k <= 2048): the 64-wide
+        // direct-to-LDS tile with sixteen stages of the reduction in flight
+        // (128 KiB of LDS), so a short product is not a chain of memory round
+        // trips, and a skinny one keeps every CU busy where the 256-wide tiles
+        // would leave most idle (kernel times: 1024^3 16.3 -> 9.0 us;
+        // 128 x 2048 x 8192 31.2 -> 13.8 us, 128 x 8192 x 8192 74.6 -> 42.5 us,
+        // 16 x 8192 x 16384 69.3 -> 41.4 us, 1024 x 1024 x 2048 23.4 -> 14.6 us
+        // against the 256-wide tile; 256 x 4096 x 4096 32.2 -> 23.4 us against
+        // the 128-wide one).  Two rounds at k = 4096 measured even, at 8192
+        // 10% slower (128 x 8192 x 16384: 82.8 against 75.0 us).
+        bm = 64;
+        UOR_HIP((launch_dl<64, 64, 2, 2, EPI_FUSED, FAST, false, 16>(A, B, out, K, 0, 1, s)));
+        if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline
+    } else if (use256 && pair == 1 && dl_variant() == DL_S4 && s4t_ok(A, B, K)) {
         bm = 256;
         UOR_HIP((launch_s4<FAST, true>(A, B, out, K, s)));
         if (route) route->operand_modes |= 1 << 4;  // direct-to-LDS pipeline

@@ -96,14 +96,14 @@ __device__ inline uint64_t dl_koff(int t, uint64_t kstep) {
 // halves, so that a stage handle (its A half) reaches its B half at a fixed
 // offset and every fragment read is a lane base plus an immediate offset
 // (DS offsets are 16 bits: the four 16 KiB A halves fit below 64 KiB).
-template <int BM, int BN>
+template <int BM, int BN, int NS = DL_NSTAGE>
 struct DlLayout {
     static_assert(BM == BN, "the B halves sit one A region above their A halves");
     static constexpr int A_BYTES = BM * DL_BK;
     static constexpr int B_BYTES = BN * DL_BK;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int BYTES = DL_NSTAGE * STAGE;
-    static constexpr int B_OFF = DL_NSTAGE * A_BYTES;  // stage handle -> its B half
+    static constexpr int BYTES = NS * STAGE;
+    static constexpr int B_OFF = NS * A_BYTES;  // stage handle -> its B half
     __device__ static inline int a_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
     __device__ static inline int b_swz(int k) { return (2 * (k & 7)) & (BN / 16 - 1); }
     __device__ static inline int b_off(int k, int x) { return k * BN + 16 * (x ^ b_swz(k)); }
@@ -149,10 +149,10 @@ __device__ inline void lds_dma16(const int8_t *g, char *lds) {
 }
 #pragma clang diagnostic pop
 
-template <int BM, int BN, int NT>
+template <int BM, int BN, int NT, int NS = DL_NSTAGE>
 __device__ inline void dl_issue(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t k0,
                                 char *stage) {
-    using L = DlLayout<BM, BN>;
+    using L = DlLayout<BM, BN, NS>;
     constexpr int PA = BM * 4 / NT, PB = BN * 4 / NT;  // 16-byte chunks per thread
     static_assert(PA >= 1 && PB >= 1, "tile too small for the workgroup");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -181,24 +181,27 @@ __device__ inline void dl_issue(const Opnd &A, const Opnd &B, uint64_t m0, uint6
     }
 }
 
-// One k-step of 64 from LDS stage `sa` (A) / `sb` (B): each wave's FM x FN
-// 32x32 blocks, two 32-deep MFMAs each.
+// One k-step's fragments of a wave: FM A and FN B operands per 32-deep half.
 template <int BM, int BN, int WM, int WN>
-__device__ inline void dl_compute(const char *sa, const char *sb,
-                                  v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
+struct DlFrag {
+    v4i af[2][BM / WM / 32];
+    v4i bf[2][BN / WN / 32];
+};
+
+// The fragment reads of one k-step of 64 from LDS stage `sa` (A) / `sb` (B).
+template <int BM, int BN, int WM, int WN>
+__device__ inline void dl_frag_read(const char *sa, const char *sb, DlFrag<BM, BN, WM, WN> &f) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     using L = DlLayout<BM, BN>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int half = lane >> 5, l32 = lane & 31;
     const int grp = lane >> 4, t16 = lane & 15;
-    v4i af[2][FM];
-    v4i bf[2][FN];
 #pragma unroll
     for (int ks = 0; ks < DL_BK / 32; ++ks) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
-            af[ks][i] = *(const v4i *)(sa + L::a_off(wm * (BM / WM) + 32 * i + l32, 2 * ks + half));
+            f.af[ks][i] = *(const v4i *)(sa + L::a_off(wm * (BM / WM) + 32 * i + l32, 2 * ks + half));
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int nb = wn * (BN / WN) + 32 * j + 16 * (grp & 1) + 8 * (t16 & 1);
@@ -207,16 +210,33 @@ __device__ inline void dl_compute(const char *sa, const char *sb,
                 (lds_v2i *)(sb + L::b_off(k, nb >> 4) + (nb & 8)));
             v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                 (lds_v2i *)(sb + L::b_off(k + 8, nb >> 4) + (nb & 8)));
-            bf[ks][j] = v4i{lo[0], lo[1], hi[0], hi[1]};
+            f.bf[ks][j] = v4i{lo[0], lo[1], hi[0], hi[1]};
         }
     }
+}
+
+// The MFMAs of one k-step: each of the wave's FM x FN 32x32 blocks, two
+// 32-deep MFMAs each.
+template <int BM, int BN, int WM, int WN>
+__device__ inline void dl_frag_mma(const DlFrag<BM, BN, WM, WN> &f, v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
 #pragma unroll
     for (int ks = 0; ks < DL_BK / 32; ++ks)
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.af[ks][i], f.bf[ks][j], acc[i][j], 0, 0, 0);
+}
+
+// One k-step of 64 from LDS stage `sa` (A) / `sb` (B): each wave's FM x FN
+// 32x32 blocks, two 32-deep MFMAs each.
+template <int BM, int BN, int WM, int WN>
+__device__ inline void dl_compute(const char *sa, const char *sb,
+                                  v16i (&acc)[BM / WM / 32][BN / WN / 32]) {
+    DlFrag<BM, BN, WM, WN> f;
+    dl_frag_read<BM, BN, WM, WN>(sa, sb, f);
+    dl_frag_mma<BM, BN, WM, WN>(f, acc);
 }
 
 // The k loop over nk steps of DL_BK, step t at kbeg + dl_koff(t, kstep): each
@@ -257,6 +277,74 @@ __device__ inline void dl_mainloop(const Opnd &A, const Opnd &B, uint64_t m0, ui
         UOR_DL_STEP(st3, st2)
     }
 #undef UOR_DL_STEP
+    wait_vm<0>();
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n < 64 known only at run time.
+__device__ inline void wait_vm_rt(int n) {
+#define UOR_VMR(N) case N: wait_vm<N>(); break;
+    switch (n) {
+        UOR_VMR(0) UOR_VMR(1) UOR_VMR(2) UOR_VMR(3) UOR_VMR(4) UOR_VMR(5) UOR_VMR(6) UOR_VMR(7)
+        UOR_VMR(8) UOR_VMR(9) UOR_VMR(10) UOR_VMR(11) UOR_VMR(12) UOR_VMR(13) UOR_VMR(14) UOR_VMR(15)
+        UOR_VMR(16) UOR_VMR(17) UOR_VMR(18) UOR_VMR(19) UOR_VMR(20) UOR_VMR(21) UOR_VMR(22) UOR_VMR(23)
+        UOR_VMR(24) UOR_VMR(25) UOR_VMR(26) UOR_VMR(27) UOR_VMR(28) UOR_VMR(29) UOR_VMR(30) UOR_VMR(31)
+        default: wait_vm<0>(); break;
+    }
+#undef UOR_VMR
+}
+
+// The same k loop on a ring of NS stages: for a tile whose product is too
+// small to hide a memory round trip behind three steps of MFMAs, every stage
+// a short reduction needs is in flight at once, and a longer one keeps
+// NS - 1 stages in flight.
+template <int BM, int BN, int WM, int WN, int NS>
+__device__ inline void dl_mainloop_ring(const Opnd &A, const Opnd &B, uint64_t m0, uint64_t n0, uint64_t kbeg,
+                                        int nk, char *lds, v16i (&acc)[BM / WM / 32][BN / WN / 32],
+                                        uint64_t kstep = DL_UNIT * DL_BK) {
+    constexpr int NT = 64 * WM * WN;
+    using L = DlLayout<BM, BN, NS>;
+    constexpr int LOADS = (BM + BN) * 4 / NT;  // global_load_lds per thread per stage
+    static_assert((NS - 2) * LOADS < 32, "the run-time wait covers vmcnt below 32");
+    if (nk <= NS) {
+        // The whole reduction fits the ring: every stage requested at once,
+        // one wait and one barrier, then the steps back to back (no barrier
+        // between them, so each step's fragment reads overlap the MFMAs
+        // before them).
+        for (int t = 0; t < nk; ++t)
+            dl_issue<BM, BN, NT, NS>(A, B, m0, n0, kbeg + dl_koff(t, kstep), lds + t * L::A_BYTES);
+        wait_vm<0>();
+        stage_barrier();
+        // Step kt + 1's fragments are read before step kt's MFMAs.
+        DlFrag<BM, BN, WM, WN> f0, f1;
+        dl_frag_read<BM, BN, WM, WN>(lds, lds + L::B_OFF, f0);
+        for (int kt = 0; kt < nk; kt += 2) {
+            if (kt + 1 < nk) dl_frag_read<BM, BN, WM, WN>(lds + (kt + 1) * L::A_BYTES,
+                                                          lds + (kt + 1) * L::A_BYTES + L::B_OFF, f1);
+            dl_frag_mma<BM, BN, WM, WN>(f0, acc);
+            if (kt + 1 >= nk) break;
+            if (kt + 2 < nk) dl_frag_read<BM, BN, WM, WN>(lds + (kt + 2) * L::A_BYTES,
+                                                          lds + (kt + 2) * L::A_BYTES + L::B_OFF, f0);
+            dl_frag_mma<BM, BN, WM, WN>(f1, acc);
+        }
+        return;
+    }
+    // Longer reductions: NS - 1 stages requested; step kt waits for stage kt
+    // (the stages after it may stay in flight), passes the barrier, refills
+    // slot (kt - 1) % NS, which every wave finished reading before it, with
+    // stage kt + NS - 1, and computes.  (Reading step kt + 1's fragments
+    // before step kt's MFMAs, which needs stage kt + 1 one step earlier,
+    // measured 6-8% slower here.)
+    for (int t = 0; t < NS - 1; ++t)
+        dl_issue<BM, BN, NT, NS>(A, B, m0, n0, kbeg + dl_koff(t, kstep), lds + t * L::A_BYTES);
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_vm_rt(min(NS - 2, nk - 1 - kt) * LOADS);
+        stage_barrier();
+        if (kt + NS - 1 < nk)
+            dl_issue<BM, BN, NT, NS>(A, B, m0, n0, kbeg + dl_koff(kt + NS - 1, kstep),
+                                     lds + ((kt + NS - 1) % NS) * L::A_BYTES);
+        char *cur = lds + (kt % NS) * L::A_BYTES;
+        dl_compute<BM, BN, WM, WN>(cur, cur + L::B_OFF, acc);
+    }
     wait_vm<0>();
 }
 
