@@ -296,12 +296,14 @@ def test_config2_deep_k_2_24(uor, dev, out, alpha, beta, encode):
 
 
 @pytest.mark.parametrize("case", ["vec", "ldc_odd", "c_offset", "beta0", "wrap_alpha", "sat_alpha",
-                                  "i16", "i64"])
+                                  "i16", "i64", "identity", "i32_edges", "alpha_2p31"])
 def test_fused_tile_epilogues(uor, dev, case):
     """The 256x256 direct-to-LDS tile (>= 256 output tiles, n a multiple of
     16) with each epilogue branch: 16-byte i32 rows (vec), an odd ldc or a C
     base off 16-byte alignment (per-element i32), beta = 0, alpha large
-    enough to saturate or wrap, and i16 / i64 outputs.  Expected values from
+    enough to saturate or wrap, and i16 / i64 outputs; the i32 output's
+    32-bit-scalar evaluation at its widest scalars and one past them, and
+    alpha = 1, beta = 0 (the sum itself).  Expected values from
     an exact float64 product (|sum| <= 512 * 2^14) and a numpy encode."""
     m = n = 4096
     k = 512
@@ -316,6 +318,12 @@ def test_fused_tile_epilogues(uor, dev, case):
         alpha, beta, encode = (1 << 12) + 7, 5, "wrapping"
     if case == "sat_alpha":
         alpha, beta, encode = (1 << 12) + 7, -5, "saturating"
+    if case == "identity":  # the exact sum stored as it is
+        alpha, beta = 1, 0
+    if case == "i32_edges":  # the widest scalars of the 32-bit evaluation
+        alpha, beta, encode = -(1 << 31), (1 << 31) - 1, "saturating"
+    if case == "alpha_2p31":  # one past them: the 64-bit evaluation
+        alpha, beta, encode = 1 << 31, -1, "wrapping"
     rng = np.random.default_rng(len(case))
     dt = {"i16": np.int16, "i32": np.int32, "i64": np.int64}[out]
     a = torch.from_numpy(rng.integers(-128, 128, m * lda).astype(np.int8)).to(dev)

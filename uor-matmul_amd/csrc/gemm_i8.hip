@@ -213,6 +213,30 @@ __device__ inline void finish_any(const OutArgs &o, char *cp, int64_t sum) {
     }
 }
 
+// enc(alpha * sum + beta * prior) into i32 for alpha and beta that fit i32:
+// two signed 32x32 -> 64 multiply-adds (v_mad_i64_i32, exact: each product is
+// below 2^62 in magnitude), then Wrapping keeps the low word and every other
+// mode clamps (encode_i128_into, acc.rs:128-150).  The general path's int64
+// products cost four 32-bit multiplies and two 64-bit multiply-adds per cell.
+// (v_mad_i64_i32 through inline assembly: the compiler spells a sign-extended
+// 32x32 -> 64 product with a uniform factor as four 32-bit multiplies.)
+__device__ __attribute__((always_inline)) inline int64_t mad_i64_i32(int32_t a, int32_t b, int64_t c) {
+    int64_t r;
+    uint64_t carry;
+    asm("v_mad_i64_i32 %0, %1, %2, %3, %4" : "=v"(r), "=s"(carry) : "v"(a), "s"(b), "v"(c));
+    return r;
+}
+
+template <bool RD>
+__device__ __attribute__((always_inline)) inline int32_t enc32_small(int32_t sum, int32_t prior, int32_t a32,
+                                                                     int32_t b32, bool wrap) {
+    const int64_t ax = mad_i64_i32(sum, a32, 0);
+    const int64_t x = RD ? mad_i64_i32(prior, b32, ax) : ax;
+    const int32_t lo = (int32_t)x, hi = (int32_t)(x >> 32);
+    const int32_t sat = (hi >> 31) ^ 0x7FFFFFFF;  // INT32_MIN below the range, INT32_MAX above
+    return (wrap || hi == (lo >> 31)) ? lo : sat;
+}
+
 // Encode one 32x32 accumulator block parked row-major in LDS (row stride 33
 // ints) into C.  Lanes 0-31 / 32-63 take columns l32 of rows 2t / 2t+1.
 // The C values of a batch are all loaded before any is stored, so their
@@ -224,6 +248,31 @@ __device__ inline void encode_block(const OutArgs &o, const int *park, uint64_t 
     if (col >= N) return;
     char *const cbase = o.base + (int64_t)col * o.cs * OB;
     const int64_t rstride = o.rs * OB;
+    if constexpr (FAST && OB == 4) {
+        if (o.alpha == (int32_t)o.alpha && o.beta == (int32_t)o.beta) {
+            const int32_t a32 = (int32_t)o.alpha, b32 = (int32_t)o.beta;
+            const bool wrap = o.mode == UOR_ENCODE_WRAPPING;
+            int32_t prior[16];
+            if (b32 != 0) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const uint64_t row = rbase + 2 * t + half;
+                    prior[t] = row < M ? *(const int32_t *)(cbase + (int64_t)row * rstride) : 0;
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int lr = 2 * t + half;
+                const uint64_t row = rbase + lr;
+                if (row >= M) continue;
+                const int32_t sum = park[lr * 33 + l32];
+                *(int32_t *)(cbase + (int64_t)row * rstride) =
+                    b32 != 0 ? enc32_small<true>(sum, prior[t], a32, b32, wrap)
+                             : enc32_small<false>(sum, 0, a32, 0, wrap);
+            }
+            return;
+        }
+    }
     if constexpr (FAST && OB <= 8) {
         int64_t prior[16];
         if (o.beta != 0) {
@@ -703,8 +752,9 @@ __device__ inline void buf_store(__amdgpu_buffer_rsrc_t r, int vo, int so, int64
 }
 
 // (Always inlined: a call would pass the uniform strides in VGPRs, which the
-// "s" constraint below cannot take.)
-template <int OB, bool RD>
+// "s" constraint below cannot take.)  SMALL: i32 output, alpha and beta in
+// i32 (enc32_small); 2: alpha = 1 and beta = 0, the exact sum itself.
+template <int OB, bool RD, int SMALL = 0>
 __device__ __attribute__((always_inline)) inline void s4_epilogue_full(const OutArgs &out, const v16i (&acc)[4][4], char *corner, int vo,
                                         int srs, int scs) {
     typedef typename std::conditional<OB == 8, int64_t, int32_t>::type P;
@@ -737,14 +787,32 @@ __device__ __attribute__((always_inline)) inline void s4_epilogue_full(const Out
         }
         S4_FENCE();
         const P (&p)[4][16] = pr[NB == 2 ? (i & 1) : 0];
+        if constexpr (SMALL == 2) {
+            static_assert(OB == 4 && !RD, "the i32 output, no prior");
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                int64_t x = (int64_t)acc[i][j][r] * out.alpha;
-                if constexpr (RD) x += (int64_t)p[j][r] * out.beta;
-                buf_store<OB>(rs, vo, offs(i, j, r), (int64_t)encode_int((i128)x, OB, out.mode));
-            }
+                for (int r = 0; r < 16; ++r) buf_store<OB>(rs, vo, offs(i, j, r), acc[i][j][r]);
+        } else if constexpr (SMALL) {
+            static_assert(OB == 4, "the i32 output");
+            const int32_t a32 = (int32_t)out.alpha, b32 = RD ? (int32_t)out.beta : 0;
+            const bool wrap = out.mode == UOR_ENCODE_WRAPPING;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    buf_store<OB>(rs, vo, offs(i, j, r),
+                                  enc32_small<RD>(acc[i][j][r], RD ? (int32_t)p[j][r] : 0, a32, b32, wrap));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    int64_t x = (int64_t)acc[i][j][r] * out.alpha;
+                    if constexpr (RD) x += (int64_t)p[j][r] * out.beta;
+                    buf_store<OB>(rs, vo, offs(i, j, r), (int64_t)encode_int((i128)x, OB, out.mode));
+                }
+        }
         S4_FENCE();
     }
 }
@@ -759,6 +827,15 @@ __device__ __attribute__((always_inline)) inline void s4_epilogue_fast(const Out
         const int srs = (int)(out.rs * OB), scs = (int)(out.cs * OB);
         char *const corner = out.base + ((int64_t)rw * out.rs + (int64_t)cw * out.cs) * OB;
         const int vo = 4 * half * srs + l32 * scs;
+        const bool small = OB == 4 && out.alpha == (int32_t)out.alpha && out.beta == (int32_t)out.beta;
+        if constexpr (OB == 4) {
+            if (small) {
+                if (out.beta != 0) s4_epilogue_full<OB, true, 1>(out, acc, corner, vo, srs, scs);
+                else if (out.alpha == 1) s4_epilogue_full<OB, false, 2>(out, acc, corner, vo, srs, scs);
+                else s4_epilogue_full<OB, false, 1>(out, acc, corner, vo, srs, scs);
+                return;
+            }
+        }
         if (out.beta != 0) s4_epilogue_full<OB, true>(out, acc, corner, vo, srs, scs);
         else s4_epilogue_full<OB, false>(out, acc, corner, vo, srs, scs);
         return;
