@@ -2251,6 +2251,30 @@ __global__ void __launch_bounds__(256) limb_combine_kernel(IArgs F, const int32_
     }
 }
 
+// The same for i16 elements (three planes): every term is far inside int64
+// (|plane| < 2^31, so |sum of planes << 8s| < 2^48; |ca (sa + sb)| and
+// ca^2 k below 2^34 at the limb route's depths, k < 2^16), so the
+// combination runs in 64-bit words instead of 128-bit ones; modular lanes
+// keep the low 32 bits either way.  cak = ca^2 k.
+__global__ void __launch_bounds__(256) limb_combine16_kernel(IArgs F, const int32_t *planes, const int64_t *sa,
+                                                             const int64_t *sb, int64_t ca, int64_t cak) {
+    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
+    if (j >= F.n) return;
+    const uint64_t cell = i * F.n + j, mn = F.m * F.n;
+    const uint64_t p0 = (uint64_t)(int64_t)planes[cell], p1 = (uint64_t)(int64_t)planes[mn + cell],
+                   p2 = (uint64_t)(int64_t)planes[2 * mn + cell];
+    const int64_t x = (int64_t)((p2 << 16) + (p1 << 8) + p0 + (uint64_t)(ca * (sa[i] + sb[j])) - (uint64_t)cak);
+    W192 w{{(uint64_t)x, x < 0 ? ~(uint64_t)0 : 0, x < 0 ? ~(uint64_t)0 : 0}};
+    char *cp = F.c + ((int64_t)i * F.crs + (int64_t)j * F.ccs) * F.ob;
+    switch (F.ob) {
+    case 1: int_finish<1>(F, cp, w); break;
+    case 2: int_finish<2>(F, cp, w); break;
+    case 4: int_finish<4>(F, cp, w); break;
+    case 8: int_finish<8>(F, cp, w); break;
+    default: int_finish<16>(F, cp, w); break;
+    }
+}
+
 struct LimbLayout {
     uint64_t acat, brev, planes, sa, sb, rest;  // byte offsets
     int nplanes;
@@ -2330,8 +2354,12 @@ static int launch_int_limb(const IArgs &F, char *sc, uint64_t have, const LimbLa
         *launches += r.launches;
     }
     const int64_t ca = L == 2 ? 128 : 128 * (1 + 256 + 65536);
-    hipLaunchKernelGGL(limb_combine_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)m), dim3(256), 0, s, F,
-                       planes, Y.nplanes, sa, sb, ca);
+    if (L == 2 && Y.nplanes == 3 && k < (1ull << 16))
+        hipLaunchKernelGGL(limb_combine16_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)m), dim3(256), 0, s,
+                           F, planes, sa, sb, ca, ca * ca * (int64_t)k);
+    else
+        hipLaunchKernelGGL(limb_combine_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)m), dim3(256), 0, s, F,
+                           planes, Y.nplanes, sa, sb, ca);
     UOR_HIP(hipGetLastError());
     *launches += 1;
     return UOR_OK;
