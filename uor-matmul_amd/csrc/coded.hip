@@ -452,31 +452,38 @@ __global__ void __launch_bounds__(256) coded_gemv_win_kernel(CodedArgs W, GemvAr
 // each column's next code window is loaded before this one is used.
 template <int MR, int D, int NCOL = 4>
 __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvArgs G) {
-    __shared__ uint32_t lut[256 * D];
-    for (int idx = threadIdx.x; idx < 256 * D; idx += 256) {
-        const uint32_t code = (uint32_t)idx / D, part = (uint32_t)idx % D;
-        uint32_t v = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v |= (uint32_t)(uint8_t)dec(W.cd, code, 4 * part + e) << (8 * e);
-        lut[idx] = v;
-    }
-    __syncthreads();
+    // CP copies of the table, entry x of copy c at word x * CP + c, lane l
+    // reading copy l % CP: the lanes of one read meet in at most 64 / CP ways
+    // on a bank, where random codes into one copy meet in 4-5.
+    constexpr int CP = 16;
+    __shared__ uint32_t lut[256 * D * CP];
     const int lane = threadIdx.x & 63;
     const uint64_t jb = ((uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * NCOL;
-    if (jb >= G.n) return;  // whole waves, after the barrier
     const uint64_t nwin = W.per_row / 16;  // one-byte codes: a row is per_row bytes
     constexpr int E = 64 * D;              // elements per 16-byte window
-    int acc[NCOL][MR];
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c)
-#pragma unroll
-        for (int r = 0; r < MR; ++r) acc[c][r] = 0;
+    // Each column's first code window is requested before the table is
+    // built, so the loads are in flight meanwhile.
     uint4 nxt[NCOL];
 #pragma unroll
     for (int c = 0; c < NCOL; ++c)
         nxt[c] = ((uint64_t)lane < nwin && jb + c < G.n)
                      ? *(const uint4 *)(W.codes + (jb + c) * W.per_row + 16 * (uint64_t)lane)
                      : uint4{0, 0, 0, 0};
+    for (int idx = threadIdx.x; idx < 256 * D; idx += 256) {
+        const uint32_t code = (uint32_t)idx / D, part = (uint32_t)idx % D;
+        uint32_t v = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v |= (uint32_t)(uint8_t)dec(W.cd, code, 4 * part + e) << (8 * e);
+#pragma unroll
+        for (int c = 0; c < CP; ++c) lut[idx * CP + c] = v;
+    }
+    __syncthreads();
+    if (jb >= G.n) return;  // whole waves, after the barrier
+    int acc[NCOL][MR];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[c][r] = 0;
     for (uint64_t wi = (uint64_t)lane; wi < nwin; wi += 64) {
         uint4 cur[NCOL];
 #pragma unroll
@@ -505,7 +512,7 @@ __global__ void __launch_bounds__(256) coded_gemv_lut_kernel(CodedArgs W, GemvAr
                 const uint32_t code = (d[q >> 2] >> (8 * (q & 3))) & 0xFFu;
 #pragma unroll
                 for (int part = 0; part < D; ++part) {
-                    const int wv = (int)lut[code * D + part];
+                    const int wv = (int)lut[(code * D + part) * CP + (lane % CP)];
 #pragma unroll
                     for (int r = 0; r < MR; ++r)
                         acc[c][r] = __builtin_amdgcn_sdot4((int)a[r][q * D + part], wv, acc[c][r], false);
