@@ -897,23 +897,29 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
     for (int d = 0; d < ND; ++d) sl[d] = 0;
     double f = 0;
     const uint16_t(*Ml)[CRT_ND16] = crt_Ml16[nmod - 1];
-    const uint16_t *inv = crt_inv[nmod - 1];
+    const uint32_t *inv = crt_inv[nmod - 1];
     // G planes' bytes at a time, the next group's loads issued before this
     // group's arithmetic (clamped to the last plane, so every load is in
     // bounds and none is conditional).  The groups stay a loop: unrolled, the
     // compiler keeps every group's residues and table rows live at once (over
     // 200 VGPRs).
-    const uint8_t *yc = y + cell;
+    // Plane l of the cell at y + l * y_plane + cell: the plane offset is
+    // uniform and formed on the scalar unit (readfirstlane), so a load costs
+    // one 64-bit add per lane instead of a 64-bit multiply-add.
+    auto plane_byte = [&](int l) -> int {
+        const uint64_t off = (uint64_t)__builtin_amdgcn_readfirstlane(l) * y_plane;
+        return y[off + cell];
+    };
     int nxt[G];
 #pragma unroll
-    for (int u = 0; u < G; ++u) nxt[u] = yc[(uint64_t)min(u, nmod - 1) * y_plane];
+    for (int u = 0; u < G; ++u) nxt[u] = plane_byte(min(u, nmod - 1));
 #pragma unroll 1
     for (int l0 = 0; l0 < nmod; l0 += G) {
         int yb[G];
 #pragma unroll
         for (int u = 0; u < G; ++u) yb[u] = nxt[u];
 #pragma unroll
-        for (int u = 0; u < G; ++u) nxt[u] = yc[(uint64_t)min(l0 + G + u, nmod - 1) * y_plane];
+        for (int u = 0; u < G; ++u) nxt[u] = plane_byte(min(l0 + G + u, nmod - 1));
 #pragma unroll
         for (int u = 0; u < G; ++u) {
             const int l = l0 + u;
