@@ -706,14 +706,16 @@ __device__ inline int residue(uint64_t m, int s, bool neg, int l, const uint8_t 
         if (r < 0) r += p;
         if (r >= p) r -= p;
     } else {
-        // m < 2^53 in three 24-bit limbs: m mod p = (m0 + (m1 mod p) 2^24 +
-        // m2 2^48) mod p, every step a reduction of a value below 2^25.
-        const float ip = crt_invpf[l];
-        const uint32_t m0 = (uint32_t)m & 0xffffffu, m1 = (uint32_t)(m >> 24) & 0xffffffu,
-                       m2 = (uint32_t)(m >> 48);
-        const uint32_t t = m0 + mod_small(m1, p, ip) * pow2[l * 256 + 24] +
-                           m2 * pow2[l * 256 + 48];
-        r = (int)mod_small(mod_small(t, p, ip) * w, p, ip);
+        // m < 2^53 is exact in a double: the quotient floor(m / p) through the
+        // reciprocal is off by at most one either way, and m - q p, whose
+        // exact value is below 2p in magnitude, comes exact out of one fma;
+        // then (m mod p) * (2^s mod p) < 2^16 reduces in single precision.
+        const double md = (double)m, pd = (double)p;
+        const double q = floor(md * crt_invp[l]);
+        double rd = fma(-q, pd, md);
+        if (rd < 0) rd += pd;
+        if (rd >= pd) rd -= pd;
+        r = (int)mod_small((uint32_t)rd * w, p, crt_invpf[l]);
     }
     int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
     if (neg) b = -b;
