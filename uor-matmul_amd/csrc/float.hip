@@ -680,47 +680,35 @@ __global__ void __launch_bounds__(256) crt_plan_kernel(const LineStat *ra, uint6
     *h = r;
 }
 
-// x mod p for x < 2^25 and p < 2^8: the single-precision quotient of such an
-// x is off by at most one, which one correction each way absorbs.
-__device__ inline uint32_t mod_small(uint32_t x, int p, float ip) {
-    int r = (int)x - (int)((float)x * ip) * p;
-    if (r < 0) r += p;
-    if (r >= p) r -= p;
-    return (uint32_t)r;
-}
-
-// Balanced int8 residue of +-m * 2^s modulo crt_mod[l] (s < 256).  An f32
-// significand (< 2^24) keeps m * (2^s mod p) below 2^32, reduced through a
-// double; an f64 one is reduced in 24-bit limbs with mod_small.
+// Balanced int8 residue of +-m * 2^s modulo crt_mod[l] (s < 256); md is
+// +-m as a double (exact: m < 2^53).  Every modulus but crt_mod[0] = 256 is
+// odd, so a quotient x / p is never a half-integer: its distance from one is
+// at least 1 / (2p) >= 2^-9, and rint of x * (1/p) is the nearest integer q
+// whenever the product's error is below that; x - q p, an integer in
+// [-(p-1)/2, (p-1)/2], is then the balanced residue, exact out of one fma.
+// An f32 significand (< 2^24) keeps x = +-m (2^s mod p) below 2^32 (error of
+// x * (1/p) below 2^-24); an f64 one is first reduced to r = +-m - q' p with
+// q' = rint(md * (1/p)) off by at most one (error below 2^-3), so |r| < 3p/2,
+// and x = r (2^s mod p), below 2^17, is then reduced in single precision
+// (error below 2^-10).
 template <bool F64>
-__device__ inline int residue(uint64_t m, int s, bool neg, int l, const uint8_t *pow2) {
-    const int p = crt_mod[l];
+__device__ inline int residue(uint64_t m, double md, int s, bool neg, int l, const uint8_t *pow2) {
     const uint32_t w = pow2[l * 256 + s];
-    int r;
     if (l == 0) {
-        r = (int)(((uint32_t)m * w) & 255);
-    } else if constexpr (!F64) {
-        const uint32_t x = (uint32_t)m * w;
-        const uint32_t q = (uint32_t)floor((double)x * crt_invp[l]);
-        r = (int)(x - q * (uint32_t)p);  // in [-p, 2p) as a 32-bit difference
-        if (r < 0) r += p;
-        if (r >= p) r -= p;
-    } else {
-        // m < 2^53 is exact in a double: the quotient floor(m / p) through the
-        // reciprocal is off by at most one either way, and m - q p, whose
-        // exact value is below 2p in magnitude, comes exact out of one fma;
-        // then (m mod p) * (2^s mod p) < 2^16 reduces in single precision.
-        const double md = (double)m, pd = (double)p;
-        const double q = floor(md * crt_invp[l]);
-        double rd = fma(-q, pd, md);
-        if (rd < 0) rd += pd;
-        if (rd >= pd) rd -= pd;
-        r = (int)mod_small((uint32_t)rd * w, p, crt_invpf[l]);
+        int b = (int)(((uint32_t)m * w) & 255);
+        b = b >= 128 ? b - 256 : b;
+        if (neg) b = -b;
+        return b == 128 ? -128 : b;  // p = 256: 128 and -128 are one residue
     }
-    int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
-    if (neg) b = -b;
-    if (b == 128) b = -128;  // p = 256: 128 and -128 are one residue
-    return b;
+    const int p = crt_mod[l];
+    if constexpr (!F64) {
+        const double x = md * (double)w;
+        return (int)fma(-rint(x * crt_invp[l]), (double)p, x);
+    } else {
+        const double r = fma(-rint(md * crt_invp[l]), (double)p, md);
+        const float x = (float)r * (float)w;
+        return (int)fmaf(-rintf(x * crt_invpf[l]), (float)p, x);
+    }
 }
 
 // Residue planes.  A (ROWS_A): plane l holds m rows of S_A max * kp bytes,
@@ -797,11 +785,17 @@ __global__ void __launch_bounds__(256) residue_kernel(const char *src, int64_t s
         }
         int8_t *dst = ROWS_A ? planes + r * ((uint64_t)s_max * kp) + (uint64_t)sl * kp + c0
                              : planes + ((uint64_t)(s_max - 1 - sl) * kp + r) * np + c0;
+        double md[4];  // +-m (0 for a cell with no residue: every residue 0)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (!ok[e]) mm[e] = 0, ng[e] = false;
+            md[e] = ng[e] ? -(double)mm[e] : (double)mm[e];
+        }
         for (int l = 0; l < nmod; ++l) {
             uint32_t wd = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int v = ok[e] ? residue<F64>(mm[e], ss[e], ng[e], l, pow2) : 0;
+                const int v = residue<F64>(mm[e], md[e], ss[e], ng[e], l, pow2);
                 wd |= (uint32_t)(uint8_t)(int8_t)v << (8 * e);
             }
             *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = wd;
