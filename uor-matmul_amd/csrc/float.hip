@@ -495,10 +495,13 @@ __device__ inline int bitlen64(uint64_t v) { return 64 - __builtin_clzll(v); }
 
 // Statistics of `lines` lines of `len` elements: element e of line t at
 // base + t * s_line + e * s_elem.  LPB lines per workgroup, thread t on line
-// t % LPB at elements t / LPB, + 256 / LPB, ...: LPB = 1 (s_elem == 1) puts
-// the threads along one line; LPB = 64 (s_line == 1) puts a wave across 64
-// neighbouring lines, one 64-element row segment per load; LPB = 16 is for
-// the other strides.
+// t % LPB at elements t / LPB, + NT / LPB, ...: LPB = 1 (s_elem == 1) puts
+// the threads along one line; LPB = 64, 16 or 4 (s_line == 1) puts a wave
+// across LPB neighbouring lines, one LPB-element row segment per lane group;
+// LPB = 16 with 256 threads is for the other strides.  One pass: each thread
+// keeps its top bit hi and the sum of its |aligned integers| scaled by
+// 2^-hi (every term at most 1), rescaled by a power of two when hi rises,
+// and the threads' pairs combine the same way.
 template <bool F64, int LPB, int NT = 256>
 __global__ void __launch_bounds__(NT) line_stats_kernel(const char *base, int64_t s_line,
                                                         int64_t s_elem, uint64_t lines,
@@ -512,6 +515,7 @@ __global__ void __launch_bounds__(NT) line_stats_kernel(const char *base, int64_
     const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
     const bool live = line < lines;
     int lo = 1 << 30, hi = -(1 << 30), fl = 0;
+    double sum = 0;
     if (live) {
         for (uint64_t e0 = te; e0 < len; e0 += (uint64_t)TPL * U) {
             uint64_t v[U];
@@ -531,20 +535,28 @@ __global__ void __launch_bounds__(NT) line_stats_kernel(const char *base, int64_
                 uint64_t m;
                 int x;
                 trim(d, &m, &x);
+                const int top = x + bitlen64(m);
                 lo = min(lo, x);
-                hi = max(hi, x + bitlen64(m));
+                if (top > hi) {
+                    sum = ldexp(sum, hi - top);
+                    hi = top;
+                }
+                sum += ldexp((double)m, x - hi);
             }
         }
     }
     s_lo[t] = lo;
     s_hi[t] = hi;
     s_fl[t] = fl;
+    s_sum[t] = sum;
     __syncthreads();
     for (int w = TPL / 2; w >= 1; w >>= 1) {
         if (te < w) {
             const int o = t + LPB * w;
+            const int h0 = s_hi[t], h1 = s_hi[o], h = max(h0, h1);
+            s_sum[t] = ldexp(s_sum[t], h0 - h) + ldexp(s_sum[o], h1 - h);
+            s_hi[t] = h;
             s_lo[t] = min(s_lo[t], s_lo[o]);
-            s_hi[t] = max(s_hi[t], s_hi[o]);
             s_fl[t] |= s_fl[o];
         }
         __syncthreads();
@@ -552,34 +564,6 @@ __global__ void __launch_bounds__(NT) line_stats_kernel(const char *base, int64_
     lo = s_lo[tl];
     hi = s_hi[tl];
     fl = s_fl[tl];
-    // Pass 2: sum of |aligned integers| scaled by 2^-(top), each term <= 1.
-    double sum = 0;
-    if (live && hi > lo) {
-        for (uint64_t e0 = te; e0 < len; e0 += (uint64_t)TPL * U) {
-            uint64_t v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint64_t e = e0 + (uint64_t)u * TPL;
-                v[u] = e < len ? load_bits<F64>(base, (int64_t)line * s_line + (int64_t)e * s_elem) : 0;
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const Dec d = decode<F64>(v[u]);
-                if (d.cls != CLS_FINITE || !d.mant) continue;
-                uint64_t m;
-                int x;
-                trim(d, &m, &x);
-                sum += ldexp((double)m, x - hi);
-            }
-        }
-    }
-    __syncthreads();
-    s_sum[t] = sum;
-    __syncthreads();
-    for (int w = TPL / 2; w >= 1; w >>= 1) {
-        if (te < w) s_sum[t] += s_sum[t + LPB * w];
-        __syncthreads();
-    }
     if (te == 0 && live) {
         LineStat st;
         if (hi <= lo) {
@@ -591,7 +575,8 @@ __global__ void __launch_bounds__(NT) line_stats_kernel(const char *base, int64_
             st.lo = lo;
             st.width = hi - lo;
             // Rounding of the double sum is below 2^-30 relative for any
-            // reachable length; terms that underflowed are below 2^-900 each.
+            // reachable length (the rescalings are exact); terms that
+            // underflowed are below 2^-900 each.
             const double s = s_sum[tl] * (1.0 + 0x1p-28) + (double)len * 0x1p-900;
             st.l1 = (float)(log2(s) + (double)(hi - lo) + 1e-6);
             st.flags = fl | (st.width > WIDE_BITS ? LS_WIDE : 0);
@@ -1448,17 +1433,23 @@ static int crt_slice_cap(bool f64, uint64_t k) {
 }
 
 // Line statistics with the lanes along a line when it is contiguous; a wave
-// across 64 neighbouring lines, 16 waves on the line's elements, when
-// neighbouring lines are neighbouring elements (B's columns); else 16 lines
-// by 16 lanes.
+// across 64, 16 or 4 neighbouring lines (the most that still makes 256
+// workgroups), 16 waves on the lines' elements, when neighbouring lines are
+// neighbouring elements (B's columns); else 16 lines by 16 lanes.
 template <bool F64>
 static void launch_line_stats(const char *base, int64_t s_line, int64_t s_elem, uint64_t lines,
                               uint64_t len, LineStat *out, hipStream_t s) {
     if (s_elem == 1)
         hipLaunchKernelGGL((line_stats_kernel<F64, 1>), dim3((unsigned)lines), dim3(256), 0, s, base, s_line,
                            s_elem, lines, len, out);
-    else if (s_line == 1)  // neighbouring lines are neighbouring elements: a wave across 64 lines
+    else if (s_line == 1 && lines >= 64 * 256)  // neighbouring lines are neighbouring elements
         hipLaunchKernelGGL((line_stats_kernel<F64, 64, 1024>), dim3((unsigned)((lines + 63) / 64)), dim3(1024), 0, s,
+                           base, s_line, s_elem, lines, len, out);
+    else if (s_line == 1 && lines >= 16 * 256)  // (fewer lines per workgroup: 256 workgroups at least)
+        hipLaunchKernelGGL((line_stats_kernel<F64, 16, 1024>), dim3((unsigned)((lines + 15) / 16)), dim3(1024), 0, s,
+                           base, s_line, s_elem, lines, len, out);
+    else if (s_line == 1)
+        hipLaunchKernelGGL((line_stats_kernel<F64, 4, 1024>), dim3((unsigned)((lines + 3) / 4)), dim3(1024), 0, s,
                            base, s_line, s_elem, lines, len, out);
     else
         hipLaunchKernelGGL((line_stats_kernel<F64, 16>), dim3((unsigned)((lines + 15) / 16)), dim3(256), 0, s,
