@@ -1604,42 +1604,45 @@ __device__ inline void w192_add(W192 &x, i128 v) {
 
 // Line statistics of integer lines: lo = 0, width = bit length of the
 // largest magnitude, l1 an upper bound of log2 of the sum of magnitudes.
-template <int EB, int LPB>
-__global__ void __launch_bounds__(256) int_line_stats_kernel(const char *base, int64_t s_line,
-                                                             int64_t s_elem, uint64_t lines,
-                                                             uint64_t len, LineStat *out) {
-    constexpr int TPL = 256 / LPB;  // threads per line (as line_stats_kernel)
-    __shared__ int s_hi[256];
-    __shared__ double s_sum[256];
+// Lines and threads as line_stats_kernel, and the same one pass: a running
+// sum scaled by 2^-hi, rescaled by a power of two when hi rises.
+template <int EB, int LPB, int NT = 256>
+__global__ void __launch_bounds__(NT) int_line_stats_kernel(const char *base, int64_t s_line,
+                                                            int64_t s_elem, uint64_t lines,
+                                                            uint64_t len, LineStat *out) {
+    constexpr int TPL = NT / LPB;  // threads per line
+    __shared__ int s_hi[NT];
+    __shared__ double s_sum[NT];
     const int t = threadIdx.x;
     const int tl = t % LPB, te = t / LPB;
     const uint64_t line = (uint64_t)blockIdx.x * LPB + tl;
     const bool live = line < lines;
     int hi = 0;
+    double sum = 0;
     if (live)
         for (uint64_t e = te; e < len; e += TPL) {
             const uint64_t v = mag64(load_ielem<EB>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
-            if (v) hi = max(hi, bitlen64(v));
+            if (!v) continue;
+            const int top = bitlen64(v);
+            if (top > hi) {
+                sum = ldexp(sum, hi - top);
+                hi = top;
+            }
+            sum += ldexp((double)v, -hi);
         }
     s_hi[t] = hi;
-    __syncthreads();
-    for (int w = TPL / 2; w >= 1; w >>= 1) {
-        if (te < w) s_hi[t] = max(s_hi[t], s_hi[t + LPB * w]);
-        __syncthreads();
-    }
-    hi = s_hi[tl];
-    double sum = 0;
-    if (live && hi > 0)
-        for (uint64_t e = te; e < len; e += TPL) {
-            const uint64_t v = mag64(load_ielem<EB>(base, (int64_t)line * s_line + (int64_t)e * s_elem));
-            if (v) sum += ldexp((double)v, -hi);
-        }
     s_sum[t] = sum;
     __syncthreads();
     for (int w = TPL / 2; w >= 1; w >>= 1) {
-        if (te < w) s_sum[t] += s_sum[t + LPB * w];
+        if (te < w) {
+            const int o = t + LPB * w;
+            const int h0 = s_hi[t], h1 = s_hi[o], h = max(h0, h1);
+            s_sum[t] = ldexp(s_sum[t], h0 - h) + ldexp(s_sum[o], h1 - h);
+            s_hi[t] = h;
+        }
         __syncthreads();
     }
+    hi = s_hi[tl];
     if (te == 0 && live) {
         LineStat st;
         st.lo = 0;
@@ -1659,41 +1662,30 @@ __global__ void __launch_bounds__(256) int_line_stats_kernel(const char *base, i
     }
 }
 
-// x mod p_l for x < 2^32.
-__device__ inline uint32_t umod_p(uint32_t x, int l) {
-    const int64_t p = crt_mod[l];
-    const int64_t q = (int64_t)floor((double)x * crt_invp[l]);
-    int64_t r = (int64_t)x - q * p;
-    if (r < 0) r += p;
-    if (r >= p) r -= p;
-    return (uint32_t)r;
-}
-
-// The balanced int8 residue of an EB-byte element v modulo crt_mod[l].
+// The balanced int8 residue of an EB-byte element v modulo crt_mod[l]; xh
+// and xl are +-(|v| >> 32) and +-(|v| mod 2^32) as doubles, signed as v
+// (EB <= 4: xh = 0, xl = v).  As for the float residues, every modulus but
+// 256 is odd, so for |x| < 2^32 (x * (1/p) errs by less than 2^-24, a
+// quotient x / p is at least 1/(2p) >= 2^-9 from a half-integer) x - p
+// rint(x / p) is the balanced residue, exact out of one fma; an i64 element
+// combines its halves' residues as rh (2^32 mod p) + rl, below 2^15 in
+// magnitude, and reduces that once more.
 template <int EB>
-__device__ inline int int_residue(int64_t v, int l) {
-    const uint64_t a = mag64(v);
-    const int p = crt_mod[l];
-    int r;
+__device__ inline int int_residue(int64_t v, double xh, double xl, int l) {
     if (l == 0) {
-        r = (int)(a & 255);
-    } else if constexpr (EB == 2) {
-        // a <= 2^15: a float quotient is off by at most one.
-        const int q = (int)((float)a * crt_invpf[l]);
-        r = (int)a - q * p;
-        if (r < 0) r += p;
-        if (r >= p) r -= p;
-    } else if constexpr (EB == 4) {
-        r = (int)umod_p((uint32_t)a, l);  // a <= 2^31
-    } else {
-        const uint32_t p32 = crt_pow2[l][32];  // 2^32 mod p
-        const uint32_t rh = umod_p((uint32_t)(a >> 32), l), rl = umod_p((uint32_t)a, l);
-        r = (int)umod_p(rh * p32 + rl, l);
+        int b = (int)(mag64(v) & 255);
+        b = b >= 128 ? b - 256 : b;
+        if (v < 0) b = -b;
+        return b == 128 ? -128 : b;  // p = 256: 128 and -128 are one residue
     }
-    int b = (l == 0) ? (r >= 128 ? r - 256 : r) : (r > p / 2 ? r - p : r);
-    if (v < 0) b = -b;
-    if (b == 128) b = -128;  // p = 256: 128 and -128 are one residue
-    return b;
+    const double p = (double)crt_mod[l], ip = crt_invp[l];
+    double x = fma(-rint(xl * ip), p, xl);
+    if constexpr (EB == 8) {
+        const double rh = fma(-rint(xh * ip), p, xh);
+        x = fma(rh, (double)crt_pow2[l][32], x);
+        x = fma(-rint(x * ip), p, x);
+    }
+    return (int)x;
 }
 
 // Residue planes of an integer operand, laid out as residue_kernel's
@@ -1718,13 +1710,26 @@ __global__ void __launch_bounds__(256) int_residue_kernel(const char *src, int64
             const uint64_t sc = c0 + e;
             v[e] = (r < rows && sc < cols) ? load_ielem<EB>(src, (int64_t)r * s_r + (int64_t)sc * s_c) : 0;
         }
+        double xh[4], xl[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (EB == 8) {
+                const uint64_t a = mag64(v[e]);
+                const double sg = v[e] < 0 ? -1.0 : 1.0;
+                xh[e] = sg * (double)(uint32_t)(a >> 32);
+                xl[e] = sg * (double)(uint32_t)a;
+            } else {
+                xh[e] = 0;
+                xl[e] = (double)v[e];
+            }
+        }
         int8_t *dst = ROWS_A ? planes + r * ((uint64_t)s_max * kp) + c0
                              : planes + ((uint64_t)(s_max - 1) * kp + r) * np + c0;
         for (int l = 0; l < nmod; ++l) {
             uint32_t wd = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                wd |= (uint32_t)(uint8_t)(int8_t)(v[e] ? int_residue<EB>(v[e], l) : 0) << (8 * e);
+                wd |= (uint32_t)(uint8_t)(int8_t)int_residue<EB>(v[e], xh[e], xl[e], l) << (8 * e);
             *(uint32_t *)(dst + (uint64_t)l * plane_bytes) = wd;
         }
     }
@@ -1885,6 +1890,15 @@ static hipError_t launch_int_crt(const IArgs &F, char *scratch, const CrtLayout 
         if (s_elem == 1)
             hipLaunchKernelGGL((int_line_stats_kernel<EB, 1>), dim3((unsigned)lines), dim3(256), 0, s, base,
                                s_line, s_elem, lines, k, out);
+        else if (s_line == 1 && lines >= 64 * 256)  // B's columns: as launch_line_stats
+            hipLaunchKernelGGL((int_line_stats_kernel<EB, 64, 1024>), dim3((unsigned)((lines + 63) / 64)),
+                               dim3(1024), 0, s, base, s_line, s_elem, lines, k, out);
+        else if (s_line == 1 && lines >= 16 * 256)
+            hipLaunchKernelGGL((int_line_stats_kernel<EB, 16, 1024>), dim3((unsigned)((lines + 15) / 16)),
+                               dim3(1024), 0, s, base, s_line, s_elem, lines, k, out);
+        else if (s_line == 1)
+            hipLaunchKernelGGL((int_line_stats_kernel<EB, 4, 1024>), dim3((unsigned)((lines + 3) / 4)),
+                               dim3(1024), 0, s, base, s_line, s_elem, lines, k, out);
         else
             hipLaunchKernelGGL((int_line_stats_kernel<EB, 16>), dim3((unsigned)((lines + 15) / 16)), dim3(256),
                                0, s, base, s_line, s_elem, lines, k, out);
