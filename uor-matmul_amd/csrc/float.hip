@@ -1810,8 +1810,12 @@ __device__ inline void int_finish(const IArgs &F, char *cp, const W192 &sum) {
     store_out<OB>(cp, v);
 }
 
+// (Always inlined: as a called function its arguments arrive in vector
+// registers, and crt16 would then read the tables indexed by nmod with vector
+// loads, each waited for, instead of on the scalar unit.)
 template <int ND>
-__device__ inline W192 crt_w192(const uint8_t *y, uint64_t y_plane, uint64_t cell, int nmod) {
+__device__ __attribute__((always_inline)) inline W192 crt_w192(const uint8_t *y, uint64_t y_plane, uint64_t cell,
+                                                               int nmod) {
     uint32_t D[ND];
     const bool neg = crt16<ND>(y, y_plane, cell, nmod, D);
     // |X| < 2^192 (B <= 192), so the digits past the twelfth are zero.
