@@ -316,6 +316,30 @@ def test_crt_plan_is_tight(oracle, uor, dev):
     assert np.array_equal(bits(c.cpu().numpy()), bits(want))
 
 
+@pytest.mark.parametrize("spread", [40, 50])
+def test_crt_fast_wide_unsliced(oracle, uor, dev, spread):
+    """Unsliced lines close to the 160-bit slicing limit (f64 significands
+    times 2^e, e in [-spread, spread]): bounds past 256 bits, so more than 33
+    moduli and more than sixteen 16-bit digits on the register finish
+    (crt_fast_kernel, beta = 0; alpha up to 65535 takes one more digit), bit
+    for bit with the oracle."""
+    rng = np.random.default_rng(spread)
+    m, k, n = 16, 48, 24
+
+    def mat(r, c):
+        mant = rng.integers(1 << 52, 1 << 53, size=r * c).astype(np.float64)
+        e = rng.integers(-spread, spread + 1, size=r * c)
+        return rng.choice([-1.0, 1.0], size=r * c) * np.ldexp(mant, e - 52)
+
+    a, b = mat(m, k), mat(k, n)
+    for alpha in (1, -3, 65535):
+        sc = offer_for(uor, dev, "full", True, m, k, n)
+        check(oracle, uor, dev, a, b, m, k, n, alpha=alpha, scratch=sc, expect_route="float_crt")
+        off = (-sc.data_ptr()) % 256
+        nmod, crt_off, need, sa, sb = sc[off:off + 20].cpu().view(torch.int32).tolist()
+        assert crt_off == 0 and sa == 1 and sb == 1 and nmod >= 34 and need > 252, (nmod, need, sa, sb)
+
+
 @pytest.mark.parametrize("is64,N", [(False, 4096), (True, 2048)])
 def test_config4_full_size_rows_and_columns(oracle, uor, dev, is64, N):
     """configs[3] at its full size: f32 4096^3 (e in [-40, 40]) and f64 2048^3

@@ -866,18 +866,23 @@ residue_gemm_kernel(uint64_t m, uint64_t n, int gm, int gn, ResOut R) {
 }
 
 // The CRT reconstruction of X_ij in ND 16-bit digits: |X| into D[] (each in
-// [0, 2^16)), returns true when X < 0.  Each slot sums at most 49 products of
-// a residue (< 2^8) and a 16-bit digit of M / p_l, below 2^30, so the sums
-// run on 24-bit multiply-adds in 32-bit lanes; the quotient round(sum c_l /
+// [0, 2^16)), returns true when X < 0.  The sum over the moduli runs in
+// 32-bit digits held in doubles: each slot adds a residue (< 2^8) times a
+// 32-bit digit of M / p_l by one fma, and 49 such products stay below 2^46,
+// so every partial sum is an exact integer.  The quotient round(sum c_l /
 // p_l) is exact in a double because |X| / M stays 2^-21 away from 1/2.
+// Digits past the tables' CRT_ND (a 16-bit digit count of ND = 2 CRT_ND - 1
+// or 2 CRT_ND, room for an alpha) are zero in M and every M / p_l.
 template <int ND, int G = 8>
 __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, int nmod,
                              uint32_t (&D)[ND]) {
-    int32_t sl[ND];
+    constexpr int NW = (ND + 1) / 2;                   // 32-bit digits
+    constexpr int NT = NW < CRT_ND ? NW : CRT_ND;      // those the tables hold
+    double sl[NT];
 #pragma unroll
-    for (int d = 0; d < ND; ++d) sl[d] = 0;
+    for (int e = 0; e < NT; ++e) sl[e] = 0;
     double f = 0;
-    const uint16_t(*Ml)[CRT_ND16] = crt_Ml16[nmod - 1];
+    const double(*Ml)[CRT_ND] = crt_Ml[nmod - 1];
     const uint32_t *inv = crt_inv[nmod - 1];
     // G planes' bytes at a time, the next group's loads issued before this
     // group's arithmetic (clamped to the last plane, so every load is in
@@ -916,21 +921,27 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
                     if (c < 0) c += p;
                     if (c >= p) c -= p;
                 }
-                f += (double)c * crt_invp[l];
+                const double cd = (double)c;
+                f += cd * crt_invp[l];
 #pragma unroll
-                for (int d = 0; d < ND; ++d)  // c < 2^8, Ml < 2^16: a 24-bit multiply
-                    sl[d] += (int32_t)__umul24((uint32_t)c, (uint32_t)Ml[l][d]);
+                for (int e = 0; e < NT; ++e) sl[e] = fma(cd, Ml[l][e], sl[e]);
             }
         }
     }
-    const int32_t q = (int32_t)floor(f + 0.5);
-    int32_t carry = 0;
+    // X = sum - q M in two's complement over NW 32-bit digits: v below 2^47
+    // in magnitude, its floor division by 2^32 and remainder exact.
+    const double q = floor(f + 0.5);
+    double carry = 0;
+    uint32_t W[NW];
 #pragma unroll
-    for (int d = 0; d < ND; ++d) {
-        const int32_t v = sl[d] - q * (int32_t)crt_M16[nmod][d] + carry;
-        D[d] = (uint32_t)(v & 0xffff);
-        carry = v >> 16;  // arithmetic: floor division
+    for (int e = 0; e < NW; ++e) {
+        const double v = (e < NT ? fma(-q, crt_M[nmod][e < NT ? e : 0], sl[e < NT ? e : 0]) : 0.0) + carry;
+        const double hi = floor(v * 0x1p-32);
+        W[e] = (uint32_t)fma(-hi, 0x1p32, v);
+        carry = hi;
     }
+#pragma unroll
+    for (int d = 0; d < ND; ++d) D[d] = (W[d / 2] >> (16 * (d % 2))) & 0xffff;
     const bool neg = carry < 0;
     if (neg) {
         uint32_t c = 1;
