@@ -867,9 +867,9 @@ residue_gemm_kernel(uint64_t m, uint64_t n, int gm, int gn, ResOut R) {
 
 // The CRT reconstruction of X_ij in ND 16-bit digits: |X| into D[] (each in
 // [0, 2^16)), returns true when X < 0.  The sum over the moduli runs in
-// 32-bit digits held in doubles: each slot adds a residue (< 2^8) times a
-// 32-bit digit of M / p_l by one fma, and 49 such products stay below 2^46,
-// so every partial sum is an exact integer.  The quotient round(sum c_l /
+// 32-bit digits held in doubles: each slot adds a residue (|c| <= 129) times
+// a 32-bit digit of M / p_l by one fma, and 49 such products stay below
+// 2^46 in magnitude, so every partial sum is an exact integer.  The quotient round(sum c_l /
 // p_l) is exact in a double because |X| / M stays 2^-21 away from 1/2.
 // Digits past the tables' CRT_ND (a 16-bit digit count of ND = 2 CRT_ND - 1
 // or 2 CRT_ND, room for an alpha) are zero in M and every M / p_l.
@@ -910,26 +910,20 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
         for (int u = 0; u < G; ++u) {
             const int l = l0 + u;
             if (l < CRT_NMAX && l < nmod) {
-                const int p = crt_mod[l];
-                const int prod = yb[u] * (int)inv[l];  // < 2^16
-                int c;
-                if (l == 0) {
-                    c = prod & 255;
-                } else {
-                    const int q = (int)((float)prod * crt_invpf[l]);
-                    c = prod - q * p;
-                    if (c < 0) c += p;
-                    if (c >= p) c -= p;
-                }
-                const double cd = (double)c;
+                // c = yb * (M / p_l)^-1 mod p_l, any representative: x - p
+                // rint(x / p), |c| <= p / 2 + 1 (x < 2^16, so x * (1/p) errs
+                // far below the rounding's half), exact out of one fma.
+                const double x = (double)(int)__umul24((uint32_t)yb[u], inv[l]);
+                const double cd = fma(-rint(x * crt_invp[l]), crt_modd[l], x);
                 f += cd * crt_invp[l];
 #pragma unroll
                 for (int e = 0; e < NT; ++e) sl[e] = fma(cd, Ml[l][e], sl[e]);
             }
         }
     }
-    // X = sum - q M in two's complement over NW 32-bit digits: v below 2^47
-    // in magnitude, its floor division by 2^32 and remainder exact.
+    // X = sum - q M in two's complement over NW 32-bit digits (q of either
+    // sign): v below 2^47 in magnitude, its floor division by 2^32 and
+    // remainder exact.
     const double q = floor(f + 0.5);
     double carry = 0;
     uint32_t W[NW];
