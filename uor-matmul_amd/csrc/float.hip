@@ -2243,18 +2243,26 @@ __global__ void __launch_bounds__(256) limb_split_b_kernel(IArgs F, int8_t *brev
     for (int q = 0; q < NJ; ++q) atomicAdd((unsigned long long *)&sb[j + q], (unsigned long long)sum[q]);
 }
 
-// One thread per cell: X from the planes and the line sums (two's-complement
-// i128 arithmetic, exact when the planes are, right mod 2^32 otherwise), then
-// Linear::finish and the encode.
-__global__ void __launch_bounds__(256) limb_combine_kernel(IArgs F, const int32_t *planes, int nplanes,
-                                                           const int64_t *sa, const int64_t *sb, int64_t ca) {
+// One thread per cell: X from the NP planes and the line sums (two's-
+// complement i128 arithmetic, exact when the planes are, right mod 2^32
+// otherwise), then Linear::finish and the encode.  NP is a template
+// argument so the plane loads are issued together (a loop over a run-time
+// count waited for each in turn); cak = ca^2 k as an i128 (lo, hi).
+template <int NP>
+__global__ void __launch_bounds__(256) limb_combine_kernel(IArgs F, const int32_t *planes, const int64_t *sa,
+                                                           const int64_t *sb, int64_t ca, uint64_t cak_lo,
+                                                           uint64_t cak_hi) {
     const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
     if (j >= F.n) return;
     const uint64_t cell = i * F.n + j, mn = F.m * F.n;
+    int32_t pv[NP];
+#pragma unroll
+    for (int sft = 0; sft < NP; ++sft) pv[sft] = planes[(uint64_t)sft * mn + cell];
     u128 x = 0;
-    for (int sft = nplanes - 1; sft >= 0; --sft) x = (x << 8) + (u128)(i128)planes[(uint64_t)sft * mn + cell];
+#pragma unroll
+    for (int sft = NP - 1; sft >= 0; --sft) x = (x << 8) + (u128)(i128)pv[sft];
     x += (u128)((i128)ca * ((i128)sa[i] + (i128)sb[j]));
-    x -= (u128)((i128)ca * (i128)ca * (i128)F.k);
+    x -= ((u128)cak_hi << 64) | (u128)cak_lo;
     const i128 v = (i128)x;
     W192 w{{(uint64_t)x, (uint64_t)(x >> 64), v < 0 ? ~(uint64_t)0 : 0}};
     char *cp = F.c + ((int64_t)i * F.crs + (int64_t)j * F.ccs) * F.ob;
@@ -2373,9 +2381,19 @@ static int launch_int_limb(const IArgs &F, char *sc, uint64_t have, const LimbLa
     if (L == 2 && Y.nplanes == 3 && k < (1ull << 16))
         hipLaunchKernelGGL(limb_combine16_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)m), dim3(256), 0, s,
                            F, planes, sa, sb, ca, ca * ca * (int64_t)k);
-    else
-        hipLaunchKernelGGL(limb_combine_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)m), dim3(256), 0, s, F,
-                           planes, Y.nplanes, sa, sb, ca);
+    else {
+        const u128 cak = (u128)((i128)ca * (i128)ca * (i128)k);
+        const dim3 grid((unsigned)((n + 255) / 256), (unsigned)m);
+        if (Y.nplanes == 3)
+            hipLaunchKernelGGL(limb_combine_kernel<3>, grid, dim3(256), 0, s, F, planes, sa, sb, ca, (uint64_t)cak,
+                               (uint64_t)(cak >> 64));
+        else if (Y.nplanes == 4)
+            hipLaunchKernelGGL(limb_combine_kernel<4>, grid, dim3(256), 0, s, F, planes, sa, sb, ca, (uint64_t)cak,
+                               (uint64_t)(cak >> 64));
+        else  // 2 L - 1 planes, L = 4
+            hipLaunchKernelGGL(limb_combine_kernel<7>, grid, dim3(256), 0, s, F, planes, sa, sb, ca, (uint64_t)cak,
+                               (uint64_t)(cak >> 64));
+    }
     UOR_HIP(hipGetLastError());
     *launches += 1;
     return UOR_OK;
