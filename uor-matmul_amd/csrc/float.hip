@@ -2209,33 +2209,46 @@ __global__ void __launch_bounds__(256) limb_split_b_kernel(IArgs F, int8_t *brev
     int64_t sum[NJ];
 #pragma unroll
     for (int q = 0; q < NJ; ++q) sum[q] = 0;
-    for (int e = 0; e < LIMB_SPLIT_B && p0 + e < F.k; ++e) {
-        const uint64_t p = p0 + e;
-        int64_t v[NJ];
-        if constexpr (VEC4) {
-            const char *src = F.b + ((int64_t)p * F.brs + (int64_t)j) * EB;
-            if constexpr (EB == 2) {
-                const uint2 x = *(const uint2 *)src;
-                v[0] = (int16_t)x.x, v[1] = (int16_t)(x.x >> 16), v[2] = (int16_t)x.y, v[3] = (int16_t)(x.y >> 16);
+    // U rows at a time, their loads issued together (rows past k read as
+    // zero and are not stored).
+    constexpr int U = 8;
+    for (int e0 = 0; e0 < LIMB_SPLIT_B && p0 + e0 < F.k; e0 += U) {
+        int64_t v[U][NJ];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t p = p0 + e0 + u;
+            const bool in = e0 + u < LIMB_SPLIT_B && p < F.k;
+            if constexpr (VEC4) {
+                const char *src = F.b + ((int64_t)p * F.brs + (int64_t)j) * EB;
+                if constexpr (EB == 2) {
+                    const uint2 x = in ? *(const uint2 *)src : uint2{0, 0};
+                    v[u][0] = (int16_t)x.x, v[u][1] = (int16_t)(x.x >> 16), v[u][2] = (int16_t)x.y,
+                    v[u][3] = (int16_t)(x.y >> 16);
+                } else {
+                    const uint4 x = in ? *(const uint4 *)src : uint4{0, 0, 0, 0};
+                    v[u][0] = (int32_t)x.x, v[u][1] = (int32_t)x.y, v[u][2] = (int32_t)x.z, v[u][3] = (int32_t)x.w;
+                }
             } else {
-                const uint4 x = *(const uint4 *)src;
-                v[0] = (int32_t)x.x, v[1] = (int32_t)x.y, v[2] = (int32_t)x.z, v[3] = (int32_t)x.w;
+                v[u][0] = in ? load_ielem<EB>(F.b, (int64_t)p * F.brs + (int64_t)j * F.bcs) : 0;
             }
-        } else {
-            v[0] = load_ielem<EB>(F.b, (int64_t)p * F.brs + (int64_t)j * F.bcs);
         }
 #pragma unroll
-        for (int q = 0; q < NJ; ++q) sum[q] += v[q];
+        for (int u = 0; u < U; ++u) {
+            const uint64_t p = p0 + e0 + u;
+            if (!(e0 + u < LIMB_SPLIT_B && p < F.k)) continue;
 #pragma unroll
-        for (int t = 0; t < L; ++t) {
-            int8_t *dst = brev + ((uint64_t)(L - 1 - t) * F.k + p) * F.n + j;
-            if constexpr (VEC4) {
-                uint32_t w = 0;
+            for (int q = 0; q < NJ; ++q) sum[q] += v[u][q];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) w |= (uint32_t)(uint8_t)limb_of<EB>(v[q], t) << (8 * q);
-                *(uint32_t *)dst = w;
-            } else {
-                *dst = limb_of<EB>(v[0], t);
+            for (int t = 0; t < L; ++t) {
+                int8_t *dst = brev + ((uint64_t)(L - 1 - t) * F.k + p) * F.n + j;
+                if constexpr (VEC4) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) w |= (uint32_t)(uint8_t)limb_of<EB>(v[u][q], t) << (8 * q);
+                    *(uint32_t *)dst = w;
+                } else {
+                    *dst = limb_of<EB>(v[u][0], t);
+                }
             }
         }
     }
