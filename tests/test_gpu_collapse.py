@@ -69,6 +69,32 @@ def test_rows(oracle, uor, dev, m, k, n, distinct):
     assert route["kind"] == "collapsed" and route["moduli"] == distinct, route
 
 
+@pytest.mark.parametrize("k", [8, 130, 200])
+def test_rows_aligned_padded(oracle, uor, dev, k):
+    """Rows that start 16 bytes apart with a stride past k (random padding):
+    the pass reads them 16 bytes at a time with a ragged tail, and the
+    padding never enters a class (the distinct count is the data's)."""
+    rng = np.random.default_rng(k)
+    m, n, distinct = 300, 40, 23
+    ld = (k + 15) // 16 * 16 + 16
+    a2 = repeated(rng, m, distinct, k)
+    buf = rng.integers(-128, 128, (m, ld)).astype(np.int8)
+    buf[:, :k] = a2
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8).reshape(-1)
+    want = np.zeros(m * n, np.int32)
+    assert oracle.gemm_int(buf.reshape(-1), (m, k), (ld, 1), b, (k, n), (n, 1), want, (m, n), (n, 1),
+                           alpha=3) == "ok"
+    ga = torch.from_numpy(buf.reshape(-1).copy()).to(dev)
+    gb = torch.from_numpy(b).to(dev)
+    gc = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    sc = torch.empty(uor.suggested_scratch_collapse(m, k, n), dtype=torch.uint8, device=dev)
+    st, route = uor.gemm_collapsed_i8(ga, (m, k), (ld, 1), gb, (k, n), (n, 1), gc, (m, n), (n, 1),
+                                      out="i32", alpha=3, scratch=sc)
+    torch.cuda.synchronize()
+    assert st == 0 and route["kind"] == "collapsed" and route["moduli"] == distinct, route
+    assert np.array_equal(gc.cpu().numpy(), want)
+
+
 def test_columns(oracle, uor, dev):
     rng = np.random.default_rng(2)
     m, k, n = 50, 77, 400

@@ -55,6 +55,27 @@ __device__ inline uint64_t row_word(const RowsArgs &R, uint64_t i, uint64_t q) {
     return w;
 }
 
+// Lines of contiguous, 16-byte aligned bytes (every line start a multiple of
+// 16): read 16 bytes per lane and step.
+__device__ inline bool rows16(const RowsArgs &R) {
+    return R.cs == 1 && ((uintptr_t)R.a & 15) == 0 && (R.rs & 15) == 0;
+}
+
+// Chunk t (16 bytes) of a whole-chunk run of row i (16t + 16 <= k).
+__device__ inline uint4 row_chunk(const RowsArgs &R, uint64_t i, uint64_t t) {
+    return *(const uint4 *)(R.a + (int64_t)i * R.rs + (int64_t)(16 * t));
+}
+
+// Words 2t and 2t + 1 of the last, partial chunk t of row i (16t < k <
+// 16t + 16; the second zero when 16t + 8 >= k, where it is not a word of the
+// row).
+__device__ inline void row_tail16(const RowsArgs &R, uint64_t i, uint64_t t, uint64_t &w0, uint64_t &w1) {
+    w0 = row_word(R, i, 16 * t);
+    w1 = 16 * t + 8 < R.k ? row_word(R, i, 16 * t + 8) : 0;
+}
+
+__device__ inline uint64_t word_key(uint64_t w) { return w * 0x9E3779B97F4A7C15ull; }
+
 // A sum of keyed word mixes: independent of how the words are split among
 // lanes.  Zero is the table's empty key, so a zero hash becomes one.
 __global__ void __launch_bounds__(256) row_hash_kernel(RowsArgs R, uint64_t *hash) {
@@ -62,7 +83,34 @@ __global__ void __launch_bounds__(256) row_hash_kernel(RowsArgs R, uint64_t *has
     const int lane = threadIdx.x & 63;
     if (i >= R.m) return;
     uint64_t h = 0;
-    for (uint64_t w = lane; 8 * w < R.k; w += 64) h += mix64(row_word(R, i, 8 * w) ^ (w * 0x9E3779B97F4A7C15ull));
+    if (rows16(R)) {
+        // The whole chunks, U per lane and step with their loads issued
+        // together; then the partial chunk, if any, by one lane.
+        constexpr int U = 4;
+        const uint64_t nfull = R.k / 16;
+        for (uint64_t t0 = lane; t0 < nfull; t0 += 64 * U) {
+            uint4 x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) x[u] = row_chunk(R, i, min(t0 + 64 * u, nfull - 1));  // (clamped: no branch)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                // (a mask, not a branch: the compiler would sink the loads
+                // into one and wait for each)
+                const uint64_t t = t0 + 64 * u, keep = (uint64_t)0 - (uint64_t)(t < nfull);
+                h += (mix64(((uint64_t)x[u].x | (uint64_t)x[u].y << 32) ^ word_key(2 * t)) +
+                      mix64(((uint64_t)x[u].z | (uint64_t)x[u].w << 32) ^ word_key(2 * t + 1))) &
+                     keep;
+            }
+        }
+        if (R.k % 16 && (uint64_t)lane == nfull % 64) {
+            uint64_t w0, w1;
+            row_tail16(R, i, nfull, w0, w1);
+            h += mix64(w0 ^ word_key(2 * nfull));
+            if (16 * nfull + 8 < R.k) h += mix64(w1 ^ word_key(2 * nfull + 1));
+        }
+    } else {
+        for (uint64_t w = lane; 8 * w < R.k; w += 64) h += mix64(row_word(R, i, 8 * w) ^ (w * 0x9E3779B97F4A7C15ull));
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) h += __shfl_xor(h, o, 64);
     if (lane == 0) hash[i] = h ? h : 1;
@@ -108,16 +156,49 @@ __global__ void __launch_bounds__(256) class_kernel(RowsArgs R, const uint64_t *
     uint64_t s = h & mask;
     for (uint64_t probes = 0; probes <= mask && key[s] != h; ++probes) s = (s + 1) & mask;
     uint64_t r = key[s] == h ? row[s] : i;
+    const bool v16 = rows16(R);
     if (r != i) {
         bool same = true;
-        for (uint64_t w = lane; 8 * w < R.k; w += 64) same &= row_word(R, i, 8 * w) == row_word(R, r, 8 * w);
+        if (v16) {
+            constexpr int U = 4;  // as row_hash_kernel
+            const uint64_t nfull = R.k / 16;
+            for (uint64_t t0 = lane; t0 < nfull; t0 += 64 * U) {
+                uint4 x[U], y[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint64_t t = min(t0 + 64 * u, nfull - 1);  // (clamped: no branch)
+                    x[u] = row_chunk(R, i, t);
+                    y[u] = row_chunk(R, r, t);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    same &= x[u].x == y[u].x && x[u].y == y[u].y && x[u].z == y[u].z && x[u].w == y[u].w;
+            }
+            if (R.k % 16 && (uint64_t)lane == nfull % 64) {
+                uint64_t a0, a1, b0, b1;
+                row_tail16(R, i, nfull, a0, a1);
+                row_tail16(R, r, nfull, b0, b1);
+                same &= a0 == b0 && a1 == b1;
+            }
+        } else {
+            for (uint64_t w = lane; 8 * w < R.k; w += 64) same &= row_word(R, i, 8 * w) == row_word(R, r, 8 * w);
+        }
         if (__any(!same)) r = i;  // a collision: its own class
     }
     uint32_t num = 0;
     if (r == i) {
         if (lane == 0) num = atomicAdd(counter, 1u);
         num = __shfl(num, 0, 64);
-        for (uint64_t q = lane; q < R.k; q += 64) compact[num * ldc + q] = R.a[(int64_t)i * R.rs + (int64_t)q * R.cs];
+        int8_t *dst = compact + num * ldc;
+        if (v16 && ((uintptr_t)compact & 15) == 0 && (ldc & 15) == 0) {
+            // 16 bytes per lane; the tail past the last whole chunk byte by byte
+            const uint64_t whole = R.k / 16;
+            const int8_t *src = R.a + (int64_t)i * R.rs;
+            for (uint64_t t = lane; t < whole; t += 64) ((uint4 *)dst)[t] = ((const uint4 *)src)[t];
+            for (uint64_t q = 16 * whole + lane; q < R.k; q += 64) dst[q] = src[q];
+        } else {
+            for (uint64_t q = lane; q < R.k; q += 64) dst[q] = R.a[(int64_t)i * R.rs + (int64_t)q * R.cs];
+        }
     }
     if (lane == 0) {
         rep[i] = (uint32_t)r;
