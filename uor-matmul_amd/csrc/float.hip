@@ -873,9 +873,14 @@ residue_gemm_kernel(uint64_t m, uint64_t n, int gm, int gn, ResOut R) {
 // p_l) is exact in a double because |X| / M stays 2^-21 away from 1/2.
 // Digits past the tables' CRT_ND (a 16-bit digit count of ND = 2 CRT_ND - 1
 // or 2 CRT_ND, room for an alpha) are zero in M and every M / p_l.
+// A chain of reconstructions over several plane sets (the window finish's
+// diagonals) passes `pre`: on entry (have_pre) the first G plane bytes of this
+// set, already loaded; on exit those of `ynext` (if not null), loaded while
+// this set's last group is summed instead of re-reading its own last plane.
 template <int ND, int G = 8>
 __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, int nmod,
-                             uint32_t (&D)[ND]) {
+                             uint32_t (&D)[ND], const uint8_t *ynext = nullptr, int *pre = nullptr,
+                             bool have_pre = false) {
     constexpr int NW = (ND + 1) / 2;                   // 32-bit digits
     constexpr int NT = NW < CRT_ND ? NW : CRT_ND;      // those the tables hold
     double sl[NT];
@@ -892,20 +897,25 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
     // Plane l of the cell at y + l * y_plane + cell: the plane offset is
     // uniform and formed on the scalar unit (readfirstlane), so a load costs
     // one 64-bit add per lane instead of a 64-bit multiply-add.
-    auto plane_byte = [&](int l) -> int {
+    auto plane_byte = [&](const uint8_t *base, int l) -> int {
         const uint64_t off = (uint64_t)__builtin_amdgcn_readfirstlane(l) * y_plane;
-        return y[off + cell];
+        return base[off + cell];
     };
     int nxt[G];
 #pragma unroll
-    for (int u = 0; u < G; ++u) nxt[u] = plane_byte(min(u, nmod - 1));
+    for (int u = 0; u < G; ++u) nxt[u] = have_pre ? pre[u] : plane_byte(y, min(u, nmod - 1));
 #pragma unroll 1
     for (int l0 = 0; l0 < nmod; l0 += G) {
         int yb[G];
 #pragma unroll
         for (int u = 0; u < G; ++u) yb[u] = nxt[u];
+        if (l0 + G < nmod || !ynext) {
 #pragma unroll
-        for (int u = 0; u < G; ++u) nxt[u] = plane_byte(min(l0 + G + u, nmod - 1));
+            for (int u = 0; u < G; ++u) nxt[u] = plane_byte(y, min(l0 + G + u, nmod - 1));
+        } else {
+#pragma unroll
+            for (int u = 0; u < G; ++u) nxt[u] = plane_byte(ynext, min(u, nmod - 1));
+        }
 #pragma unroll
         for (int u = 0; u < G; ++u) {
             const int l = l0 + u;
@@ -920,6 +930,10 @@ __device__ inline bool crt16(const uint8_t *y, uint64_t y_plane, uint64_t cell, 
                 for (int e = 0; e < NT; ++e) sl[e] = fma(cd, Ml[l][e], sl[e]);
             }
         }
+    }
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < G; ++u) pre[u] = nxt[u];
     }
     // X = sum - q M in two's complement over NW 32-bit digits (q of either
     // sign): v below 2^47 in magnitude, its floor division by 2^32 and
@@ -1253,6 +1267,7 @@ __device__ inline void crt_window_cell(const FArgs &F, const LineStat &sa, const
     if (hd.nmod > 0 && !((sa.flags | sb.flags) & LS_EMPTY) && F.alpha != 0) {
         const int ndiag = hd.sa + hd.sb - 1;
         const int qw = hd.w >> 5, r = hd.w & 31;
+        int pre[8];  // the next diagonal's first plane bytes (crt16's chain)
         for (int dg = ndiag - 1; dg >= 0; --dg) {
             if (dg != ndiag - 1) {
                 // T <<= w: whole words by stages of 4, 2 and 1, then r bits.
@@ -1276,8 +1291,9 @@ __device__ inline void crt_window_cell(const FArgs &F, const LineStat &sa, const
                 }
             }
             uint32_t D[ND];
-            const bool negx = crt16<ND>(y + (uint64_t)dg * nm * y_plane, y_plane, i * F.n + j,
-                                        hd.nmod, D);
+            const bool negx = crt16<ND>(y + (uint64_t)dg * nm * y_plane, y_plane, i * F.n + j, hd.nmod, D,
+                                        dg > 0 ? y + (uint64_t)(dg - 1) * nm * y_plane : nullptr, pre,
+                                        dg != ndiag - 1);
             // T += (-1)^negx X, two's complement over the whole window.
             const uint32_t xm = negx ? 0xffffffffu : 0u;
             uint32_t c = negx ? 1u : 0u;
