@@ -316,6 +316,20 @@ def test_crt_plan_is_tight(oracle, uor, dev):
     assert np.array_equal(bits(c.cpu().numpy()), bits(want))
 
 
+@pytest.mark.parametrize("is64", [False, True])
+def test_crt_all_lines_empty(oracle, uor, dev, is64):
+    """Every row of A zero (a plan with no moduli, not the direct loop): the
+    register finish still writes every cell, +0 over a nonzero C with beta =
+    0, as the oracle does."""
+    ft = np.float64 if is64 else np.float32
+    m, k, n = 8, 32, 16
+    rng = np.random.default_rng(7)
+    a = np.zeros(m * k, ft)
+    b = rng.standard_normal(k * n).astype(ft)
+    c0 = rng.standard_normal(m * n).astype(ft)
+    check(oracle, uor, dev, a, b, m, k, n, c0=c0, offer="full")
+
+
 @pytest.mark.parametrize("spread", [40, 50])
 def test_crt_fast_wide_unsliced(oracle, uor, dev, spread):
     """Unsliced lines close to the 160-bit slicing limit (f64 significands
